@@ -1,0 +1,217 @@
+"""Decode throughput of the dense-decoder token loop on one MI355X, with the Q4_K
+dequant-matvec roofline and the float64 CPU path timed beside it.
+
+Workload: the Llama-3-8B-shaped random-init Q4_K_M GGUF (32 layers, hidden 4096, 32/8
+heads, FFN 14336, vocab 128256; Q4_K attention/FFN, Q6_K attn_v and output). A 512-token
+prompt is prefilled in 128-token batches (dequant-GEMM on MFMA), then W warmup and K
+timed greedy decode steps run on the device (one HIP-graph replay per token). A step is
+one token: forward of one token through every layer plus the head and argmax.
+
+roofline: the Q4_K dequant-matvec at the 14336x4096 FFN shape (ne0 = 14336 inputs,
+4096 outputs), timed with a HIP event pair around every launch on the library's stream,
+rotating 24 distinct weight copies (~800 MB, far beyond the 256 MB Infinity Cache) so the
+bytes come from HBM. achieved = algorithmic bytes (weights + 4*in + 4*out) / mean launch
+time. The other microbench shapes (4096x4096, 4096x14336 Q4_K; 4096x128256 Q6_K) are
+reported under "matvec".
+
+cpu_baseline: the float64 C oracle (OpenMP over the host cores) decoding the same 8B
+model on a bounded sample (8-token prompt, then as many greedy tokens as fit ~15 s).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from webgpu_amd import synth  # noqa: E402
+from webgpu_amd.engine import LoadOptions, PagedEngine  # noqa: E402
+from webgpu_amd.gguf import Q4_K, Q6_K, QUANTS  # noqa: E402
+from webgpu_amd.gpu import Compute  # noqa: E402
+
+PEAK_HBM = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
+METRIC = "decode tok/s (1 GPU) + Q4_K matvec HBM GB/s as % of peak"
+
+
+class Events:
+    """hipEvent pairs on a given stream (the library's own)."""
+
+    def __init__(self) -> None:
+        self.hip = C.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self, n: int):
+        evs = []
+        for _ in range(n):
+            e = C.c_void_p()
+            assert self.hip.hipEventCreate(C.byref(e)) == 0
+            evs.append(e)
+        return evs
+
+    def record(self, e, stream) -> None:
+        assert self.hip.hipEventRecord(e, stream) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, evs) -> None:
+        for e in evs:
+            self.hip.hipEventDestroy(e)
+
+
+def matvec_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, launches: int = 96) -> dict:
+    q = QUANTS[type_]
+    wbytes = rows * cols // q["block"] * q["bytes"]
+    copies = max(2, min(24, int(800e6 // wbytes) + 1))
+    rng = np.random.default_rng(cols * 7 + rows)
+    gen = synth.microbench_q4k if type_ == Q4_K else synth.microbench_q6k
+    base = gen(rng, rows, cols)
+    ws = []
+    for i in range(copies):
+        data = base if i == 0 else np.roll(base, 144 * i * 7)  # distinct bytes per copy
+        ws.append(gpu.upload_weights(type_, cols, rows, data, f"w{i}"))
+    x = gpu.upload(rng.standard_normal(cols).astype(np.float32), "x")
+    y = gpu.buffer(rows * 4, "y")
+    stream = gpu.stream
+    for i in range(copies):  # warm: builds nothing, faults nothing, checks the path
+        gpu.matmul(type_, ws[i], x, y, cols, rows, rows, 0, 0, 1)
+    gpu.done()
+    evs = ev.create(2 * launches)
+    for i in range(launches):
+        ev.record(evs[2 * i], stream)
+        gpu.matmul(type_, ws[i % copies], x, y, cols, rows, rows, 0, 0, 1)
+        ev.record(evs[2 * i + 1], stream)
+    gpu.done()
+    times = [ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) * 1e-3 for i in range(launches)]
+    ev.destroy(evs)
+    for w in ws:
+        gpu.destroy(w)
+    gpu.destroy(x)
+    gpu.destroy(y)
+    alg = wbytes + 4 * cols + 4 * rows
+    mean = float(np.mean(times))
+    return {"shape": f"{cols}x{rows}", "type": q["name"], "bytes": alg, "us": mean * 1e6,
+            "median_us": float(np.median(times)) * 1e6, "GBps": alg / mean / 1e9, "frac": alg / mean / PEAK_HBM,
+            "copies": copies}
+
+
+def cpu_baseline(f: np.ndarray, seconds: float = 15.0) -> dict:
+    from oracle import orc
+    from webgpu_amd.context import attention_memory
+    from webgpu_amd.gguf import model_config, parse_gguf_header
+    g = parse_gguf_header(f, f.size)
+    c = model_config(g)
+    m = orc.OracleModel(f, g, c, 1024, attention_memory(c, 1024, 128)["capacities"])
+    ids = synth.prompt_ids(c.vocab, 8)
+    logits = m.forward(ids, 0)
+    tok, pos, n, t0 = int(np.argmax(logits)), 8, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n < 2:
+        logits = m.forward([tok], pos)
+        tok, pos, n = int(np.argmax(logits)), pos + 1, n + 1
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"value": n / dt, "unit": "tok/s", "cores": orc.threads(), "kind": "port",
+            "sample": f"float64 C oracle, Llama-3-8B-shaped Q4_K_M decode: 8-token prompt then {n} greedy tokens "
+                      f"in {dt:.1f} s on {orc.threads()} threads ({platform.processor() or platform.machine()})"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-matvec", action="store_true", help="skip the matvec microbench")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the token loop runs on a single MI355X (multi-GPU sharding is a design "
+              "only); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    context = 1024
+    if a.prompt + a.warmup + a.steps > context:
+        context = min(32768, 1 << (a.prompt + a.warmup + a.steps - 1).bit_length())
+
+    t = time.perf_counter()
+    f = synth.build("llama3-8b")
+    print(f"[bench] synthetic 8B GGUF {f.size / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s", file=sys.stderr, flush=True)
+    eng = PagedEngine()
+    t = time.perf_counter()
+    eng.load(f, LoadOptions(contextLength=context, batchSize=128))
+    print(f"[bench] loaded in {time.perf_counter() - t:.1f} s on {eng.gpu.adapterName}", file=sys.stderr, flush=True)
+    ids = synth.prompt_ids(eng.config.vocab, a.prompt, seed=7)
+
+    # prefill (reported, not the metric)
+    eng.gpu.done()
+    t = time.perf_counter()
+    for i in range(0, a.prompt, 128):
+        chunk = ids[i:i + 128]
+        if i + len(chunk) == a.prompt:
+            token = eng.forward_argmax(chunk, i)
+        else:
+            eng.forward(chunk, i, False)
+    eng.gpu.done()
+    prefill_s = time.perf_counter() - t
+    print(f"[bench] prefill {a.prompt} tokens in {prefill_s * 1e3:.1f} ms", file=sys.stderr, flush=True)
+
+    pos = a.prompt
+    if a.warmup:
+        warm = eng.decode(token, pos, a.warmup)
+        token, pos = warm[-1], pos + a.warmup
+    eng.gpu.done()
+    t0 = time.perf_counter()
+    toks = eng.decode(token, pos, a.steps)
+    eng.gpu.done()
+    dt = time.perf_counter() - t0
+    value = a.steps / dt
+    print(f"[bench] decode {a.steps} tokens in {dt * 1e3:.1f} ms -> {value:.1f} tok/s", file=sys.stderr, flush=True)
+
+    result = {
+        "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": dt * 1e3 / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded random-init Q4_K_M GGUF)",
+        "config": {"workload": "llama3-8b-shape Q4_K_M greedy decode", "prompt": a.prompt, "prefill_batch": 128,
+                   "decode_tokens": a.steps, "context": context, "kv_cache": "f32",
+                   "layers": 32, "hidden": 4096, "heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256},
+        "prefill_tok_s": a.prompt / prefill_s,
+    }
+    eng.dispose()
+
+    if not a.no_matvec:
+        gpu = Compute().init()
+        ev = Events()
+        shapes = [(Q4_K, 14336, 4096), (Q4_K, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 4096, 128256)]
+        mv = [matvec_bench(gpu, ev, *s) for s in shapes]
+        gpu.dispose()
+        head = mv[0]
+        result["roofline"] = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                              "frac": head["frac"], "traffic": None,
+                              "kernel": f"k_matvec<Q4K> {head['shape']} (in x out), {head['bytes']} B per launch",
+                              "mean_us": head["us"]}
+        result["matvec"] = mv
+        for m in mv:
+            print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
+                  f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+    if not a.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(f)
+        print(f"[bench] cpu baseline {result['cpu_baseline']['value']:.3f} tok/s", file=sys.stderr, flush=True)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

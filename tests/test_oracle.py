@@ -1,0 +1,281 @@
+"""Pins the float64 oracle before it is trusted as the checker.
+
+Known answers from the reference's own tests (tests/quant.test.ts:6-49), an independent
+library (numpy's IEEE half), independent numpy formulations (complex rotation, softmax),
+and invariants that a dropped term, swapped index or wrong sign would break.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import orc
+from tests import npref
+from webgpu_amd import synth
+from webgpu_amd.context import attention_memory
+from webgpu_amd.gguf import Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, F16, F32, QUANTS, model_config, parse_gguf_header
+
+
+# ---------------------------------------------------------------- quant.test.ts:6-10
+def test_half_known_answers():
+    assert orc.half(0x3C00) == 1.0 and orc.half(0xC000) == -2.0
+    assert orc.half(1) == 2.0 ** -24 and orc.half(0x7C00) == math.inf
+    assert math.isnan(orc.half(0x7E00))
+
+
+def test_half_matches_ieee_for_every_pattern():
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float64)
+    got = np.array([orc.half(int(b)) for b in bits])
+    both_nan = np.isnan(ref) & np.isnan(got)
+    assert np.array_equal(ref[~both_nan], got[~both_nan]) and np.array_equal(np.isnan(ref), np.isnan(got))
+
+
+# ---------------------------------------------------------------- quant.test.ts:11-18
+def test_q4_0_and_q8_0_signed_blocks_across_block_boundary():
+    q4 = np.zeros(36, np.uint8)
+    q4[1] = q4[19] = 0x3C
+    for i in range(16):
+        q4[2 + i] = q4[20 + i] = i | (15 - i) << 4
+    for i in range(64):
+        assert orc.decode(q4, Q4_0, i) == (i % 16 - 8 if i % 32 < 16 else 7 - i % 16)
+    q8 = np.zeros(68, np.uint8)
+    q8[1] = q8[35] = 0x3C
+    for i in range(32):
+        q8[2 + i] = q8[36 + i] = (240 + i) & 0xFF  # Uint8Array wraps, as in the reference test
+    for i in range(64):
+        assert orc.decode(q8, Q8_0, i) == i % 32 - 16
+
+
+# ---------------------------------------------------------------- quant.test.ts:19-31
+@pytest.mark.parametrize("type_", [Q4_K, Q5_K])
+def test_k_quants_recover_packed_scales_and_minima(type_):
+    data = np.zeros(144 if type_ == Q4_K else 176, np.uint8)
+    data[1] = data[3] = 0x3C
+    scales, mins = [1, 17, 35, 63, 49, 21, 38, 54], [62, 34, 18, 2, 57, 43, 29, 15]
+    for s in range(8):
+        if s < 4:
+            data[4 + s] = scales[s]
+            data[8 + s] = mins[s]
+        else:
+            data[8 + s] = (scales[s] & 15) | ((mins[s] & 15) << 4)
+            data[s] |= (scales[s] >> 4) << 6
+            data[4 + s] |= (mins[s] >> 4) << 6
+    base = 16 if type_ == Q4_K else 48
+    for group in range(4):
+        for lane in range(32):
+            data[base + group * 32 + lane] = (lane & 15) | ((15 - (lane & 15)) << 4)
+    if type_ == Q5_K:
+        data[16:48] = 0xA5
+    for i in range(256):
+        s = i // 32
+        q = (15 - i % 16 if s % 2 else i % 16) + (16 if type_ == Q5_K and ((0xA5 >> s) & 1) else 0)
+        assert orc.decode(data, type_, i) == scales[s] * q - mins[s]
+
+
+# ---------------------------------------------------------------- quant.test.ts:32-45
+def test_q6_k_reconstructs_interleaved_quarters_and_signed_scales():
+    data = np.zeros(420, np.uint8)
+    expected = np.zeros(512)
+    for block in range(2):
+        base = block * 210
+        data[base + 209] = 0x3C
+        for j in range(16):
+            data[base + 192 + j] = (j - 8) & 0xFF
+        for i in range(256):
+            value = (i * 7 + block) % 64
+            seg, qtr, lane = i // 128, (i % 128) // 32, i % 32
+            data[base + seg * 64 + qtr % 2 * 32 + lane] |= (value & 15) << ((qtr // 2) * 4)
+            data[base + 128 + seg * 32 + lane] |= (value >> 4) << (qtr * 2)
+            expected[block * 256 + i] = (value - 32) * (i // 16 - 8)
+    for i in range(512):
+        assert orc.decode(data, Q6_K, i) == expected[i]
+
+
+# ---------------------------------------------------------------- quant.test.ts:46-49
+def test_greedy_sampling_skips_non_finite():
+    assert orc.argmax(np.array([np.nan, -2, 7, 3], np.float32)) == 2
+    assert orc.argmax(np.array([np.nan, -np.inf], np.float32)) == -1
+    assert orc.argmax(np.array([1, 5, 5, -np.inf, np.inf], np.float32)) == 1  # first of equal maxima
+
+
+# ---------------------------------------------------------------- block decode vs element decode
+@pytest.mark.parametrize("type_", [F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K])
+def test_block_decoder_equals_element_decoder(type_):
+    rng = np.random.default_rng(type_)
+    q = QUANTS[type_]
+    n = 4 * max(q["block"], 64)
+    nb = n // q["block"]
+    data = np.frombuffer(rng.bytes(nb * q["bytes"]), np.uint8).copy()
+    if type_ == F32:
+        data = rng.standard_normal(n).astype(np.float32).view(np.uint8).copy()
+    block = orc.dequant(data, type_, n, f32=False)
+    elem = np.array([orc.decode(data, type_, i) for i in range(n)])
+    nan = np.isnan(elem)
+    assert np.array_equal(np.isnan(block), nan)
+    assert np.array_equal(block[~nan], elem[~nan])
+
+
+def test_f32_rounding_of_decoded_weights_is_a_single_rounding():
+    # Every product in the decode is exact, so f32(decode) is the correctly rounded value.
+    rng = np.random.default_rng(3)
+    data = synth.q4k_blocks(rng, 64)
+    d64 = orc.dequant(data, Q4_K, 64 * 256, f32=False)
+    d32 = orc.dequant(data, Q4_K, 64 * 256, f32=True)
+    assert np.array_equal(d64.astype(np.float32), d32)
+
+
+# ---------------------------------------------------------------- matmul semantics
+@pytest.mark.parametrize("type_", [F32, Q4_K, Q6_K, Q8_0])
+def test_matmul_output_offsets_against_numpy(type_):
+    rng = np.random.default_rng(11)
+    rows, cols, batch = 5, 256, 3
+    q = QUANTS[type_]
+    if type_ == F32:
+        w = rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8).copy()
+    else:
+        gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+        w = gen(rng, rows * cols // q["block"])
+    x = rng.standard_normal((batch + 1) * cols).astype(np.float32)
+    y = orc.matmul(type_, w, x, cols, rows, rows + 2, 2, 1, batch)
+    W = orc.dequant(w, type_, rows * cols, f32=False).reshape(rows, cols)
+    X = x.astype(np.float64).reshape(batch + 1, cols)[1:]
+    ref = np.zeros_like(y)
+    for b in range(batch):
+        ref[b * (rows + 2) + 2: b * (rows + 2) + 2 + rows] = W @ X[b]
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- norm / rope / attention
+def test_norm_closed_form():
+    x = np.full(64, -3.0)
+    w = np.linspace(0.5, 1.5, 64)
+    y = orc.norm(x, w, 1e-5)
+    np.testing.assert_allclose(y, -3.0 / math.sqrt(9.0 + 1e-5) * w, rtol=1e-14)
+
+
+def test_rope_matches_complex_rotation_and_pairings():
+    rng = np.random.default_rng(5)
+    heads, hd, start, batch, theta, scale, rot = 3, 16, 7, 2, 10000.0, 0.5, 12
+    x = rng.standard_normal(batch * heads * hd)
+    half = orc.rope(x, None, heads, hd, start, theta, scale, 0.0, rot, batch, 1)
+    adj = orc.rope(x, None, heads, hd, start, theta, scale, 0.0, rot, batch, 2)
+    X = x.reshape(batch, heads, hd)
+    for t in range(batch):
+        ang = (start + t) * scale / theta ** (np.arange(rot // 2) * 2 / rot)
+        e = np.exp(1j * ang)
+        # half-split: pair (i, i + rot/2) as the complex number a + ib
+        z = (X[t, :, :rot // 2] + 1j * X[t, :, rot // 2:rot]) * e
+        ref = X[t].copy()
+        ref[:, :rot // 2], ref[:, rot // 2:rot] = z.real, z.imag
+        np.testing.assert_allclose(half.reshape(batch, heads, hd)[t], ref, rtol=1e-12, atol=1e-12)
+        za = (X[t, :, 0:rot:2] + 1j * X[t, :, 1:rot:2]) * e
+        refa = X[t].copy()
+        refa[:, 0:rot:2], refa[:, 1:rot:2] = za.real, za.imag
+        np.testing.assert_allclose(adj.reshape(batch, heads, hd)[t], refa, rtol=1e-12, atol=1e-12)
+    # position 0 with scale 1 is the identity
+    np.testing.assert_allclose(orc.rope(x, None, heads, hd, 0, theta, 1.0, 0, 0, 1, 1)[:heads * hd], x[:heads * hd])
+
+
+def test_rope_qk_norm_normalises_tail_without_rotating_it():
+    rng = np.random.default_rng(9)
+    heads, hd, rot = 2, 32, 8
+    x = rng.standard_normal(heads * hd)
+    w = 1 + rng.uniform(-0.1, 0.1, hd)
+    y = orc.rope(x, w, heads, hd, 17, 1e7, 1.0, 1e-6, rot, 1, 0)
+    normed = np.concatenate([orc.norm(x[h * hd:(h + 1) * hd], w, 1e-6) for h in range(heads)])
+    rotated = orc.rope(normed, None, heads, hd, 17, 1e7, 1.0, 0, rot, 1, 1)
+    np.testing.assert_allclose(y, rotated, rtol=1e-12, atol=1e-12)
+    assert not np.allclose(y.reshape(heads, hd)[:, :rot], normed.reshape(heads, hd)[:, :rot])
+
+
+def _softmax_attention(q, k, v, heads, kvh, hd, start, scale, window, batch):
+    """Independent formulation: explicit key list per query, scipy-free stable softmax."""
+    out = np.zeros((batch, heads, hd))
+    Q = q.reshape(batch, heads, hd)
+    for b in range(batch):
+        end = start + b + 1
+        keys = list(range(max(0, end - window), end))
+        for h in range(heads):
+            kh = h // (heads // kvh)
+            s = np.array([Q[b, h] @ k[t, kh] for t in keys]) * scale
+            p = np.exp(s - s.max())
+            out[b, h] = (p / p.sum()) @ np.stack([v[t, kh] for t in keys])
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("window", [2, 5, 64])
+def test_attention_against_softmax_formulation(window):
+    rng = np.random.default_rng(window)
+    heads, kvh, hd, start, batch, ctx = 4, 2, 8, 3, 2, 16
+    q = rng.standard_normal(batch * heads * hd)
+    k = rng.standard_normal((ctx, kvh, hd))
+    v = rng.standard_normal((ctx, kvh, hd))
+    y = orc.attention(q, k.reshape(-1), v.reshape(-1), heads, kvh, hd, start, 0.3, window, ctx, batch)
+    np.testing.assert_allclose(y, _softmax_attention(q, k, v, heads, kvh, hd, start, 0.3, window, batch), rtol=1e-12)
+
+
+def test_attention_special_cases_and_ring_equivalence():
+    rng = np.random.default_rng(1)
+    heads, kvh, hd, batch = 2, 1, 8, 3
+    k = rng.standard_normal((64, kvh, hd))
+    v = rng.standard_normal((64, kvh, hd))
+    q = rng.standard_normal(batch * heads * hd)
+    # window 1: each query sees only its own key -> output is its V row
+    y = orc.attention(q, k.reshape(-1), v.reshape(-1), heads, kvh, hd, 10, 0.5, 1, 64, batch).reshape(batch, heads, hd)
+    for b in range(batch):
+        np.testing.assert_allclose(y[b, 0], v[10 + b, 0], rtol=1e-14)
+    # identical keys -> uniform weights -> mean of the visible V rows
+    ks = np.tile(k[:1], (64, 1, 1))
+    y = orc.attention(q, ks.reshape(-1), v.reshape(-1), heads, kvh, hd, 20, 0.5, 7, 64, 1).reshape(heads, hd)
+    np.testing.assert_allclose(y[1], v[14:21, 0].mean(0), rtol=1e-12)
+    # a ring of capacity window + batch - 1 holds exactly what a linear cache holds
+    start, window, cap = 40, 9, 9 + batch - 1
+    ring_k, ring_v = np.zeros((cap, kvh, hd)), np.zeros((cap, kvh, hd))
+    for t in range(start + batch - cap, start + batch):
+        ring_k[t % cap], ring_v[t % cap] = k[t], v[t]
+    lin = orc.attention(q, k.reshape(-1), v.reshape(-1), heads, kvh, hd, start, 0.5, window, 64, batch)
+    ring = orc.attention(q, ring_k.reshape(-1), ring_v.reshape(-1), heads, kvh, hd, start, 0.5, window, cap, batch)
+    np.testing.assert_allclose(ring, lin, rtol=1e-14)
+
+
+# ---------------------------------------------------------------- whole model
+def _tiny_model():
+    f = synth.build("tiny")
+    g = parse_gguf_header(f, f.size)
+    c = model_config(g)
+    caps = attention_memory(c, 512, 128)["capacities"]
+    return f, g, c, caps
+
+
+def test_tiny_forward_matches_independent_prefix_recompute():
+    f, g, c, caps = _tiny_model()
+    m = orc.OracleModel(f, g, c, 512, caps)
+    ids = synth.prompt_ids(c.vocab, 8)
+    logits = m.forward(ids, 0)
+    ref = npref.forward(f, g, c, ids)
+    np.testing.assert_allclose(logits, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_batched_prefill_equals_token_by_token():
+    f, g, c, caps = _tiny_model()
+    ids = synth.prompt_ids(c.vocab, 12, seed=3)
+    a = orc.OracleModel(f, g, c, 512, caps)
+    la = a.forward(ids[:7], 0)
+    la = a.forward(ids[7:], 7)
+    b = orc.OracleModel(f, g, c, 512, caps)
+    for i, t in enumerate(ids):
+        lb = b.forward([t], i)
+    np.testing.assert_allclose(la, lb, rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("variant", ["llama-bias-gate", "qwen3-qknorm-partial", "gemma3"])
+def test_model_variants_match_independent_forward(variant):
+    f, g, c = npref.variant_file(variant)
+    caps = attention_memory(c, 256, 8)["capacities"]
+    m = orc.OracleModel(f, g, c, 256, caps)
+    ids = synth.prompt_ids(c.vocab, 11, seed=5)
+    m.forward(ids[:8], 0)
+    logits = m.forward(ids[8:], 8)
+    ref = npref.forward(f, g, c, ids)
+    np.testing.assert_allclose(logits, ref, rtol=1e-10, atol=1e-12)

@@ -1,0 +1,73 @@
+// decode.h — device-side GGUF element decode and wavefront reductions shared by the
+// kernels of libwgd (header-only so every translation unit inlines them).
+#pragma once
+#include "internal.h"
+
+namespace wgd {
+
+__device__ __forceinline__ uint32_t block_size_dev(int t) { return t == Q6_K || t == Q4_K || t == Q5_K ? 256u : (t == Q8_0 || t == Q4_0 ? 32u : 1u); }
+
+// ------------------------------------------------------------------ exact decode
+
+// IEEE half -> float from the bit fields (quant.ts:2-5); exact for subnormals.
+__device__ __forceinline__ float half_bits(uint32_t h) {
+  uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 31u, f = h & 1023u;
+  if (e == 0) { float v = (float)f * 5.9604644775390625e-8f; return sign ? -v : v; }
+  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (f << 13));
+  return __uint_as_float(sign | ((e + 112u) << 23) | (f << 13));
+}
+__device__ __forceinline__ uint32_t byte_at(const uint8_t *b, uint64_t p) { return b[p]; }
+__device__ __forceinline__ float f16_at(const uint8_t *b, uint64_t p) {
+  return half_bits(b[p] | ((uint32_t)b[p + 1] << 8));
+}
+
+// One element of a GGUF tensor, evaluated in f32 in the reference's operation order.
+__device__ __forceinline__ float deq_elem(int type, const uint8_t *b, uint64_t i) {
+  switch (type) {
+    case F32: return __uint_as_float(b[4 * i] | (b[4 * i + 1] << 8) | (b[4 * i + 2] << 16) | ((uint32_t)b[4 * i + 3] << 24));
+    case F16: return f16_at(b, 2 * i);
+    case Q4_0: {
+      uint64_t p = (i / 32) * 18; uint32_t j = i % 32;
+      return f16_at(b, p) * (float)((int)((byte_at(b, p + 2 + j % 16) >> ((j / 16) * 4)) & 15u) - 8);
+    }
+    case Q8_0: {
+      uint64_t p = (i / 32) * 34;
+      return f16_at(b, p) * (float)(int8_t)byte_at(b, p + 2 + i % 32);
+    }
+    case Q4_K: case Q5_K: {
+      uint64_t p = (i / 256) * (type == Q4_K ? 144 : 176); uint32_t j = i % 256, s = j / 32;
+      uint32_t sc, mn;
+      if (s < 4) { sc = byte_at(b, p + 4 + s) & 63u; mn = byte_at(b, p + 8 + s) & 63u; }
+      else {
+        sc = (byte_at(b, p + 8 + s) & 15u) | ((byte_at(b, p + s) >> 6) << 4);
+        mn = (byte_at(b, p + 8 + s) >> 4) | ((byte_at(b, p + 4 + s) >> 6) << 4);
+      }
+      uint32_t q = (byte_at(b, p + (type == Q4_K ? 16 : 48) + (j / 64) * 32 + j % 32) >> ((s % 2) * 4)) & 15u;
+      if (type == Q5_K) q |= ((byte_at(b, p + 16 + j % 32) >> s) & 1u) << 4;
+      return f16_at(b, p) * (float)(sc * q) - f16_at(b, p + 2) * (float)mn;
+    }
+    case Q6_K: {
+      uint64_t p = (i / 256) * 210; uint32_t j = i % 256, seg = j / 128, qtr = (j % 128) / 32, ln = j % 32;
+      uint32_t lo = (byte_at(b, p + seg * 64 + (qtr % 2) * 32 + ln) >> ((qtr / 2) * 4)) & 15u;
+      uint32_t hi = (byte_at(b, p + 128 + seg * 32 + ln) >> (qtr * 2)) & 3u;
+      float sc = (float)(int8_t)byte_at(b, p + 192 + seg * 8 + qtr * 2 + ln / 16);
+      return f16_at(b, p + 208) * sc * (float)((int)(lo | (hi << 4)) - 32);
+    }
+  }
+  return __uint_as_float(0x7fc00000u);
+}
+
+// ------------------------------------------------------------------ wave reduction
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Sum within aligned segments of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float segment_sum(float v, int width) {
+  for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace wgd

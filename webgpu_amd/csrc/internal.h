@@ -1,0 +1,112 @@
+// internal.h — shared declarations of libwgd (gfx950). Kernel launchers take raw device
+// pointers and a stream; the C-ABI layer (runtime.hip) and the native decoder step
+// (model.hip) both call them.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/wgd.h"
+
+namespace wgd {
+
+// GGUF quantization ids (gguf.ts:6-11).
+enum QType : int { F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14 };
+
+inline int block_size(int t) {
+  switch (t) { case F32: case F16: return 1; case Q4_0: case Q8_0: return 32;
+    case Q4_K: case Q5_K: case Q6_K: return 256; }
+  return 0;
+}
+inline int block_bytes(int t) {
+  switch (t) { case F32: return 4; case F16: return 2; case Q4_0: return 18; case Q8_0: return 34;
+    case Q4_K: return 144; case Q5_K: return 176; case Q6_K: return 210; }
+  return 0;
+}
+inline uint64_t row_bytes(int t, uint64_t cols) { return cols / block_size(t) * block_bytes(t); }
+
+// Device layouts of a weight matrix. GGUF keeps the file's block bytes. The planar
+// layouts split each block's fields into 16-byte-aligned planes (same bytes, same
+// decoded values) so 210-byte Q6_K and 34-byte Q8_0 blocks can be read with aligned
+// vector loads; the planes are laid out one after another in one allocation.
+enum Layout : int { LAYOUT_GGUF = 0, LAYOUT_PLANAR = 1 };
+
+struct Matrix {
+  const uint8_t *data = nullptr;
+  int type = F32;
+  int layout = LAYOUT_GGUF;
+  uint32_t cols = 0, rows = 0;
+};
+
+// Planar plane offsets for a matrix of nb blocks.
+struct Q6Planes { uint64_t ql, qh, sc, d; };
+__host__ __device__ inline Q6Planes q6_planes(uint64_t nb) { return {0, nb * 128, nb * 192, nb * 208}; }
+struct Q8Planes { uint64_t qs, d; };
+__host__ __device__ inline Q8Planes q8_planes(uint64_t nb) { return {0, nb * 32}; }
+
+// Rewrites GGUF blocks into the planar layout (device to device).
+hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint64_t blocks);
+bool has_planar(int type);
+
+// ---------------------------------------------------------------- launchers
+// Fused-norm hook for matvec prologues: when norm_w is non-null the activation row is
+// replaced by x * inverseSqrt(mean(x^2) + eps) * norm_w before the product (the
+// normShader of shaders.ts:55-68 folded into the consumer).
+struct NormIn { const float *w = nullptr; float eps = 0.f; };
+
+// y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]
+hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
+                  uint32_t row_base, uint32_t input_offset, uint32_t batch, NormIn norm = {});
+// Batch-1 fast path with a residual epilogue: y[r] += sum_c W[r][c] x[c].
+hipError_t matmul_add(hipStream_t s, const Matrix &w, const float *x, float *y);
+hipError_t matmul_generic(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
+                          uint32_t row_base, uint32_t input_offset, uint32_t batch);
+hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
+                uint32_t row_base, uint32_t input_offset, uint32_t batch);
+// Two matrices with identical shape applied to the same (normalised) input, combined
+// by the gated activation: y = act(Wg x) * (Wu x). act 0 = SiLU, 1 = GELU-tanh.
+hipError_t matvec_glu(hipStream_t s, const Matrix &wg, const Matrix &wu, const float *x, float *y,
+                      int act, NormIn norm);
+bool fast_matvec_ok(const Matrix &w);
+
+hipError_t dequant(hipStream_t s, int type, const uint8_t *w, float *out, uint64_t count);
+hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *ids, float *out,
+                 uint32_t hidden, uint32_t n, double scale);
+hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_t n, float eps,
+                uint32_t batch);
+// mode 0: Q/K norm + half-split, 1: half-split, 2: adjacent pairs. start_dev overrides start.
+hipError_t rope(hipStream_t s, float *x, const float *w, uint32_t heads, uint32_t hd,
+                uint32_t start, const int32_t *start_dev, float theta, float scale, float eps,
+                uint32_t rotary_dim, uint32_t batch, int mode);
+struct AttnArgs {
+  const float *q; const float *k; const float *v; float *y;
+  uint32_t heads, kv_heads, hd, start; const int32_t *start_dev;
+  float scale; uint32_t window, capacity, batch;
+  float *partial; uint32_t partial_floats;  // split-K scratch (may be null: single split)
+};
+hipError_t attention(hipStream_t s, const AttnArgs &a);
+uint64_t attention_scratch_floats(uint32_t heads, uint32_t hd, uint32_t batch, uint32_t max_keys);
+hipError_t add(hipStream_t s, const float *delta, float *state, uint32_t n);
+hipError_t glu(hipStream_t s, const float *gate, const float *up, float *y, uint32_t n, int act);
+hipError_t bias_add(hipStream_t s, float *y, const float *b, uint32_t n, uint32_t width);
+hipError_t activate(hipStream_t s, float *x, uint32_t n);
+// argmax over finite values, first index wins; writes -1 when none is finite.
+hipError_t argmax(hipStream_t s, const float *logits, uint32_t n, int32_t *out);
+// Copies K/V rows of a batch into ring slots (start + i) % capacity.
+hipError_t kv_append(hipStream_t s, const float *k, const float *v, float *kc, float *vc,
+                     uint32_t row_floats, uint32_t n, uint32_t start, const int32_t *start_dev,
+                     uint32_t capacity);
+// Normalise `delta` with w (post-norm) and add into state: state += norm(delta) * w.
+hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n,
+                    float eps, uint32_t batch);
+
+int device_cu_count();
+
+}  // namespace wgd
+
+#define WGD_HIP(expr)                         \
+  do {                                        \
+    hipError_t _e = (expr);                   \
+    if (_e != hipSuccess) return _e;          \
+  } while (0)

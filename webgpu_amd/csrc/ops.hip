@@ -1,0 +1,227 @@
+// ops.hip — RMSNorm, RoPE (Q/K-norm + half-split, half-split, adjacent), residual add,
+// SwiGLU / GeGLU, bias, SiLU, KV ring append and greedy argmax for gfx950.
+//
+// Semantics follow src/core/shaders.ts: normShader :55-68, ropeShader :69-87,
+// ropeNeoxShader :139-152, ropeClassicShader :155-168, addShader :123-128,
+// geluShader :129-137, biasAddShader :170-175, activateShader :177-181, siluShader
+// (src/core/qwen-shaders.ts:27-34), the KV copies of engine.ts:120-124 / context.ts:34-37
+// and sample(T=0) of engine.ts:305-309. RoPE angles are formed in f64
+// (pos * scale * theta^(-2i/rot)) with f64 sin/cos so long positions track the f64 oracle.
+#include "internal.h"
+#include "decode.h"
+
+namespace wgd {
+
+// ------------------------------------------------------------------ block reduction
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+  v = wave_sum(v);
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// ------------------------------------------------------------------ RMSNorm
+__global__ __launch_bounds__(256) void k_norm(const float *x, const float *w, float *y, uint32_t n, float eps) {
+  __shared__ float red[4];
+  const float *xr = x + (uint64_t)blockIdx.x * n;
+  float *yr = y + (uint64_t)blockIdx.x * n;
+  float s = 0.f;
+  for (uint32_t i = threadIdx.x; i < n; i += 256) { float v = xr[i]; s += v * v; }
+  s = block_sum_256(s, red);
+  float inv = 1.f / sqrtf(s / (float)n + eps);
+  for (uint32_t i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * inv * w[i];
+}
+
+hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_t n, float eps, uint32_t batch) {
+  if (!batch || !n) return hipSuccess;
+  hipLaunchKernelGGL(k_norm, dim3(batch), dim3(256), 0, s, x, w, y, n, eps);
+  return hipGetLastError();
+}
+
+// state += norm(delta) * w (Gemma 3 post-attention / post-FFN norms, engine.ts:165-166,172-173)
+__global__ __launch_bounds__(256) void k_norm_add(const float *d, const float *w, float *state, uint32_t n, float eps) {
+  __shared__ float red[4];
+  const float *dr = d + (uint64_t)blockIdx.x * n;
+  float *sr = state + (uint64_t)blockIdx.x * n;
+  float s = 0.f;
+  for (uint32_t i = threadIdx.x; i < n; i += 256) { float v = dr[i]; s += v * v; }
+  s = block_sum_256(s, red);
+  float inv = 1.f / sqrtf(s / (float)n + eps);
+  for (uint32_t i = threadIdx.x; i < n; i += 256) sr[i] += dr[i] * inv * w[i];
+}
+
+hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n, float eps, uint32_t batch) {
+  if (!batch || !n) return hipSuccess;
+  hipLaunchKernelGGL(k_norm_add, dim3(batch), dim3(256), 0, s, delta, w, state, n, eps);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ RoPE
+// One wavefront per (token, head). mode 0: per-head RMS with w, then half-split rotation of
+// the first rot dims, tail normalised only; 1: half-split; 2: adjacent pairs.
+__global__ __launch_bounds__(256) void k_rope(float *x, const float *w, uint32_t heads, uint32_t hd,
+                                              uint32_t start, const int32_t *start_dev, float theta,
+                                              float scale, float eps, uint32_t rot, uint32_t batch,
+                                              int mode) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= heads * batch) return;
+  const uint32_t t = item / heads;
+  float *v = x + (uint64_t)item * hd;
+  const uint32_t s0 = start_dev ? (uint32_t)*start_dev : start;
+  float inv = 1.f;
+  if (mode == 0) {
+    float s = 0.f;
+    for (uint32_t i = lane; i < hd; i += 64) s += v[i] * v[i];
+    s = wave_sum(s);
+    inv = 1.f / sqrtf(s / (float)hd + eps);
+  }
+  const double pos = (double)(s0 + t) * (double)scale;
+  const uint32_t half = rot / 2;
+  for (uint32_t i = lane; i < half; i += 64) {
+    double angle = pos * pow((double)theta, -(double)(2 * i) / (double)rot);
+    double sn, cs;
+    sincos(angle, &sn, &cs);
+    float c = (float)cs, sf = (float)sn;
+    uint32_t ia = mode == 2 ? 2 * i : i, ib = mode == 2 ? 2 * i + 1 : i + half;
+    float a = v[ia], b = v[ib];
+    if (mode == 0) { a = a * w[ia] * inv; b = b * w[ib] * inv; }
+    v[ia] = a * c - b * sf;
+    v[ib] = a * sf + b * c;
+  }
+  if (mode == 0)
+    for (uint32_t i = rot + lane; i < hd; i += 64) v[i] = v[i] * w[i] * inv;
+}
+
+hipError_t rope(hipStream_t s, float *x, const float *w, uint32_t heads, uint32_t hd, uint32_t start,
+                const int32_t *start_dev, float theta, float scale, float eps, uint32_t rotary_dim,
+                uint32_t batch, int mode) {
+  if (!batch || !heads) return hipSuccess;
+  uint32_t rot = rotary_dim ? rotary_dim : hd;
+  uint32_t items = heads * batch;
+  hipLaunchKernelGGL(k_rope, dim3((items + 3) / 4), dim3(256), 0, s, x, w, heads, hd, start, start_dev, theta,
+                     scale, eps, rot, batch, mode);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ elementwise
+__global__ void k_add(const float *d, float *state, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) state[i] += d[i];
+}
+__device__ __forceinline__ float gelu_tanh_f(float g) {
+  return 0.5f * g * (1.f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g)));
+}
+__global__ void k_glu(const float *g, const float *u, float *y, uint32_t n, int act) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    float x = g[i];
+    y[i] = (act ? gelu_tanh_f(x) : x / (1.f + expf(-x))) * u[i];
+  }
+}
+__global__ void k_bias(float *y, const float *b, uint32_t n, uint32_t width) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) y[i] += b[i % width];
+}
+__global__ void k_activate(float *x, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) { float v = x[i]; x[i] = v / (1.f + expf(-v)); }
+}
+
+static dim3 grid_for(uint32_t n) { uint32_t g = (n + 255) / 256; if (g > 4096) g = 4096; if (!g) g = 1; return dim3(g); }
+
+hipError_t add(hipStream_t s, const float *delta, float *state, uint32_t n) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_add, grid_for(n), dim3(256), 0, s, delta, state, n);
+  return hipGetLastError();
+}
+hipError_t glu(hipStream_t s, const float *gate, const float *up, float *y, uint32_t n, int act) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_glu, grid_for(n), dim3(256), 0, s, gate, up, y, n, act);
+  return hipGetLastError();
+}
+hipError_t bias_add(hipStream_t s, float *y, const float *b, uint32_t n, uint32_t width) {
+  if (!n) return hipSuccess;
+  if (!width) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_bias, grid_for(n), dim3(256), 0, s, y, b, n, width);
+  return hipGetLastError();
+}
+hipError_t activate(hipStream_t s, float *x, uint32_t n) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_activate, grid_for(n), dim3(256), 0, s, x, n);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ KV ring append
+__global__ void k_kv_append(const float *k, const float *v, float *kc, float *vc, uint32_t row, uint32_t n,
+                            uint32_t start, const int32_t *start_dev, uint32_t capacity) {
+  const uint32_t s0 = start_dev ? (uint32_t)*start_dev : start;
+  const uint64_t total = (uint64_t)n * row;
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
+    uint32_t t = (uint32_t)(i / row), e = (uint32_t)(i % row);
+    uint64_t slot = (uint64_t)((s0 + t) % capacity) * row + e;
+    kc[slot] = k[i];
+    vc[slot] = v[i];
+  }
+}
+
+hipError_t kv_append(hipStream_t s, const float *k, const float *v, float *kc, float *vc, uint32_t row_floats,
+                     uint32_t n, uint32_t start, const int32_t *start_dev, uint32_t capacity) {
+  if (!n) return hipSuccess;
+  if (!capacity) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_kv_append, grid_for(n * row_floats), dim3(256), 0, s, k, v, kc, vc, row_floats, n, start,
+                     start_dev, capacity);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ argmax
+// Key = (order-preserving bits of the value) << 32 | (~index): the largest key is the
+// largest finite value with the lowest index. Non-finite entries never produce a key, so
+// key 0 means "no finite logit".
+__device__ __forceinline__ uint64_t arg_key(float f, uint32_t i) {
+  if (!isfinite(f)) return 0;
+  uint32_t u = f == 0.f ? 0u : __float_as_uint(f);
+  uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - i);
+}
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t lo = __shfl_xor((uint32_t)k, o, 64), hi = __shfl_xor((uint32_t)(k >> 32), o, 64);
+    k = key_max(k, ((uint64_t)hi << 32) | lo);
+  }
+  return k;
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const float *x, uint32_t n, uint64_t *part) {
+  __shared__ uint64_t red[4];
+  uint64_t k = 0;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) k = key_max(k, arg_key(x[i], i));
+  k = wave_max_key(k);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = key_max(key_max(red[0], red[1]), key_max(red[2], red[3]));
+}
+__global__ __launch_bounds__(256) void k_argmax_final(const uint64_t *part, uint32_t np, int32_t *out) {
+  __shared__ uint64_t red[4];
+  uint64_t k = 0;
+  for (uint32_t i = threadIdx.x; i < np; i += 256) k = key_max(k, part[i]);
+  k = wave_max_key(k);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t m = key_max(key_max(red[0], red[1]), key_max(red[2], red[3]));
+    *out = m ? (int32_t)(0xFFFFFFFFu - (uint32_t)m) : -1;
+  }
+}
+
+// Scratch for the partial keys lives right after the int32 result (out must point into
+// a buffer of at least 8 + 8 * 256 bytes, 8-byte aligned past out).
+hipError_t argmax(hipStream_t s, const float *logits, uint32_t n, int32_t *out) {
+  uint32_t blocks = (n + 4095) / 4096; if (blocks > 256) blocks = 256; if (!blocks) blocks = 1;
+  uint64_t *part = (uint64_t *)((uint8_t *)out + 8);
+  hipLaunchKernelGGL(k_argmax_partial, dim3(blocks), dim3(256), 0, s, logits, n, part);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, part, blocks, out);
+  return hipGetLastError();
+}
+
+}  // namespace wgd

@@ -1,0 +1,311 @@
+"""``PagedEngine``: host mirror of ``src/core/engine.ts`` driving the native decoder.
+
+The public surface follows the reference engine (engine.ts:26-324): ``load`` →
+``ModelInfo``, ``generate`` → TokenEvents, ``reset``, ``dispose``, ``info`` and the
+greedy ``sample``. GGUF parsing, configuration and KV-ring sizing run on the host exactly
+as in gguf.ts/context.ts; weights are uploaded once and stay resident (the pager of
+pager.ts collapses), and each forward / decode step runs inside libwgd on the GPU.
+
+Tokenizers are not part of this runtime: ``generate`` takes prompt token ids, or any
+object with ``chat(messages) -> ids``, ``decode(ids) -> str`` and ``eos`` (the shape of
+the reference's tokenizers) passed as ``tokenizer``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import mmap
+import os
+import time
+from dataclasses import dataclass, field
+from typing import Any, Dict, Iterator, List, Optional, Sequence
+
+import numpy as np
+
+from .context import MAX_CONTEXT, attention_memory, output_limit, validate_context
+from .gguf import GGUF, ModelConfig, Tensor, model_config, read_gguf
+from .gpu import Compute, ModelConfigC, WgdError, lib
+
+BATCHES = (1, 8, 16, 32, 64, 128)
+
+
+class ByteSource:
+    """Random-access bytes (source.ts:2-6) over a file (mmap) or an in-memory buffer."""
+
+    def __init__(self, data, name: str = "model.gguf") -> None:
+        self._mm = None
+        if isinstance(data, (str, os.PathLike)):
+            self.name = os.path.basename(str(data))
+            fd = os.open(str(data), os.O_RDONLY)
+            try:
+                size = os.fstat(fd).st_size
+                if size < 24:
+                    raise ValueError("Invalid model file size.")
+                self._mm = mmap.mmap(fd, size, prot=mmap.PROT_READ)
+            finally:
+                os.close(fd)
+            self._view = np.frombuffer(self._mm, np.uint8)
+        else:
+            self.name = name
+            self._view = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data.reshape(-1).view(np.uint8)
+        self.size = int(self._view.size)
+        if self.size < 24:
+            raise ValueError("Invalid model file size.")
+
+    def read(self, offset: int, length: int) -> np.ndarray:
+        if offset < 0 or length < 1 or offset + length > self.size:
+            raise ValueError("Invalid model byte range.")
+        return self._view[offset:offset + length]
+
+    def close(self) -> None:
+        self._view = None
+        if self._mm is not None:
+            self._mm.close()
+            self._mm = None
+
+
+@dataclass
+class LoadOptions:
+    contextLength: int = 512
+    batchSize: int = 128
+    gpuBudgetMiB: Optional[int] = None
+    device: int = 0
+
+
+@dataclass
+class GenerationOptions:
+    maxTokens: int = 128
+    temperature: float = 0.0
+
+
+@dataclass
+class TokenEvent:
+    token: int
+    text: str
+    delta: str
+    tokens: int
+    promptTokens: int
+    contextLength: int
+    seconds: float
+    stats: Dict[str, Any] = field(default_factory=dict)
+
+
+@dataclass
+class ModelInfo:
+    config: ModelConfig
+    fileBytes: int
+    adapter: str
+    contextLength: int
+    batchSize: int
+    stats: Dict[str, Any]
+
+
+def _config_struct(c: ModelConfig, context: int, batch: int) -> ModelConfigC:
+    s = ModelConfigC()
+    gemma = c.family == "gemma3"
+    s.family = 1 if gemma else 0
+    s.rope_adjacent = 1 if c.rope == "norm" else 0
+    s.hidden, s.intermediate, s.layers = c.hidden, c.intermediate, c.layers
+    s.heads, s.kv_heads, s.head_dim, s.vocab = c.heads, c.kvHeads, c.headDim, c.vocab
+    s.rotary_dim = c.rotaryDim
+    s.window = c.window if gemma else c.slidingWindow
+    s.period = c.period
+    s.qk_norm = 1 if c.qkNorm else 0
+    s.ffn_gate = 1 if c.ffnGate else 0
+    s.gelu = 1 if c.activation == "gelu" else 0
+    s.bias_q, s.bias_k, s.bias_v, s.bias_output = (1 if c.bias[k] else 0 for k in ("q", "k", "v", "output"))
+    s.context, s.batch = context, batch
+    s.epsilon, s.theta, s.local_theta = c.epsilon, c.theta, c.localTheta
+    s.attention_scale, s.rope_scale = c.attentionScale, c.ropeScale
+    s.embed_scale = math.sqrt(c.hidden) if c.architecture == "gemma3" else 1.0
+    return s
+
+
+class PagedEngine:
+    """The dense-decoder engine with every weight resident on one MI355X."""
+
+    def __init__(self, progress=None) -> None:
+        self.progress = progress or (lambda p: None)
+        self.gpu: Optional[Compute] = None
+        self.model: Optional[int] = None
+        self.source: Optional[ByteSource] = None
+        self.gguf: Optional[GGUF] = None
+        self.config: Optional[ModelConfig] = None
+        self.context = 512
+        self.batch = 128
+        self.kvCapacities: List[int] = []
+        self.busy = False
+        self.disposed = False
+        self.tokensInCache: List[int] = []
+
+    # ------------------------------------------------------------------ load
+    def load(self, source, options: Optional[LoadOptions] = None) -> ModelInfo:
+        """PagedEngine.load (engine.ts:51-114): parse, configure, upload, seal."""
+        o = options or LoadOptions()
+        self.context, self.batch = o.contextLength, o.batchSize
+        validate_context(self.context)
+        if self.batch not in BATCHES:
+            raise ValueError("Batch size must be 1, 8, 16, 32, 64 or 128.")
+        if o.gpuBudgetMiB is not None and (not isinstance(o.gpuBudgetMiB, int) or o.gpuBudgetMiB < 512):
+            raise ValueError("GPU budget must be at least 512 MiB.")
+        self.source = source if isinstance(source, ByteSource) else ByteSource(source)
+        self.progress({"phase": "loading", "detail": "Reading GGUF metadata", "fraction": 0.05})
+        self.gguf = read_gguf(self.source)
+        self.config = c = model_config(self.gguf)
+        validate_context(self.context, c.maxContext)
+        memory = attention_memory(c, self.context, self.batch)
+        self.kvCapacities = list(memory["capacities"])
+        self.gpu = Compute(o.gpuBudgetMiB, o.device)
+        try:
+            self.gpu.init()
+            cfg = _config_struct(c, self.context, self.batch)
+            cfg.tied_output = 0 if "output.weight" in self.gguf.tensors else 1
+            caps = (C.c_int32 * c.layers)(*self.kvCapacities)
+            out = C.c_void_p()
+            self.gpu.check(lib().wgd_model_create(self.gpu.ctx, C.byref(cfg), caps, C.byref(out)))
+            self.model = out.value
+            tensors = [t for t in self.gguf.tensors.values()
+                       if len(t.dims) in (1, 2) and (not t.name.startswith("blk.") or int(t.name.split(".")[1]) < c.layers)]
+            for i, t in enumerate(tensors):
+                self._upload(t)
+                if i % 64 == 0:
+                    self.progress({"phase": "loading", "detail": "Uploading weights", "fraction": 0.1 + 0.85 * i / len(tensors)})
+            self.gpu.check(lib().wgd_model_ready(self.model))
+            self.progress({"phase": "ready", "detail": "Ready.", "fraction": 1.0})
+            return self.info()
+        except Exception:
+            self.dispose()
+            raise
+
+    def _upload(self, t: Tensor) -> None:
+        data = self.source.read(t.offset, t.bytes)
+        dims = (C.c_uint64 * len(t.dims))(*t.dims)
+        self.gpu.check(lib().wgd_model_tensor(self.model, t.name.encode(), t.type, len(t.dims), dims,
+                                              data.ctypes.data, t.bytes))
+
+    def info(self) -> ModelInfo:
+        return ModelInfo(self.config, self.source.size if self.source else 0, self.gpu.adapterName if self.gpu else "",
+                         self.context, self.batch, self.stats())
+
+    def stats(self) -> Dict[str, Any]:
+        return {"gpuBytes": self.gpu.allocated if self.gpu else 0, "peakGpuBytes": self.gpu.peak if self.gpu else 0}
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, ids: Sequence[int], start: int, logits: bool) -> Optional[np.ndarray]:
+        """forward(ids, start, logits) (engine.ts:138-180): returns the last row's logits."""
+        if self.model is None:
+            raise RuntimeError("Load a model first.")
+        n = len(ids)
+        arr = (C.c_int32 * n)(*ids)
+        out = np.empty(self.config.vocab, np.float32) if logits else None
+        self.gpu.check(lib().wgd_model_forward(self.model, arr, n, start,
+                                               out.ctypes.data if logits else None, None))
+        return out
+
+    def forward_argmax(self, ids: Sequence[int], start: int) -> int:
+        """forward + sample(T=0) with the argmax taken on the device."""
+        n = len(ids)
+        arr = (C.c_int32 * n)(*ids)
+        tok = C.c_int32(-1)
+        self.gpu.check(lib().wgd_model_forward(self.model, arr, n, start, None, C.byref(tok)))
+        return tok.value
+
+    def decode(self, token: int, start: int, count: int) -> List[int]:
+        """``count`` greedy steps on the device from ``token`` at ``start``."""
+        out = (C.c_int32 * count)()
+        self.gpu.check(lib().wgd_model_decode(self.model, token, start, count, out))
+        return list(out)
+
+    # ------------------------------------------------------------------ generate
+    def generate(self, prompt, options: Optional[GenerationOptions] = None, tokenizer=None,
+                 chunk: int = 32) -> Iterator[TokenEvent]:
+        """PagedEngine.generate (engine.ts:257-301) with greedy sampling.
+
+        Prefix reuse, output limit, chunked prefill and the busy guard follow the
+        reference; the decode loop runs on the device ``chunk`` tokens at a time."""
+        if self.busy:
+            raise RuntimeError("A generation is already running.")
+        if self.disposed or self.model is None:
+            raise RuntimeError("Load a model first.")
+        o = options or GenerationOptions()
+        if not isinstance(o.maxTokens, int) or o.maxTokens < 1 or o.maxTokens > MAX_CONTEXT:
+            raise ValueError(f"maxTokens must be 1–{MAX_CONTEXT}.")
+        if o.temperature != 0:
+            raise ValueError("Only greedy decoding (temperature 0) is implemented by this runtime.")
+        ids = list(tokenizer.chat(prompt)) if tokenizer is not None else [int(t) for t in prompt]
+        if not ids:
+            raise ValueError("Provide a non-empty prompt.")
+        eos = set(getattr(tokenizer, "eos", ()) or ())
+        self.busy = True
+        return self._generate(ids, o, tokenizer, eos, max(1, chunk))
+
+    def _generate(self, prompt: List[int], o: GenerationOptions, tokenizer, eos, chunk: int) -> Iterator[TokenEvent]:
+        try:
+            limit = output_limit(o.maxTokens, len(prompt), self.context)
+            shared = 0
+            while shared < len(prompt) and shared < len(self.tokensInCache) and prompt[shared] == self.tokensInCache[shared]:
+                shared += 1
+            shared = min(shared, len(prompt) - 1)
+            if shared < len(self.tokensInCache) and any(cap < self.context for cap in self.kvCapacities):
+                shared = 0
+            started = time.perf_counter()
+            self.tokensInCache = self.tokensInCache[:shared]
+            token = -1
+            for i in range(shared, len(prompt), self.batch):
+                batch = prompt[i:i + self.batch]
+                last = i + len(batch) == len(prompt)
+                if last:
+                    token = self.forward_argmax(batch, i)
+                else:
+                    self.forward(batch, i, False)
+                self.tokensInCache.extend(batch)
+            generated: List[int] = []
+            text = ""
+            pending: List[int] = []
+            for i in range(limit):
+                if not pending and i > 0:
+                    count = min(chunk, limit - i)
+                    pending = self.decode(token, len(self.tokensInCache), count)
+                    # decode fed `token` and the first count-1 outputs; they enter the
+                    # cache as they are yielded below.
+                    self.tokensInCache.append(token)
+                    token = pending.pop(0)
+                elif i > 0:
+                    self.tokensInCache.append(token)
+                    token = pending.pop(0)
+                if token in eos:
+                    break
+                generated.append(token)
+                full = tokenizer.decode(generated) if tokenizer is not None else ""
+                delta = full[len(text):]
+                text = full
+                yield TokenEvent(token, text, delta, len(generated), len(prompt), self.context,
+                                 time.perf_counter() - started, self.stats())
+        except BaseException:
+            self.tokensInCache = []
+            raise
+        finally:
+            self.busy = False
+
+    def reset(self) -> None:
+        if self.busy:
+            raise RuntimeError("Stop generation first.")
+        self.tokensInCache = []
+
+    def dispose(self) -> None:
+        self.disposed = True
+        if self.model is not None and self.gpu is not None and self.gpu.ctx:
+            lib().wgd_model_destroy(self.model)
+        self.model = None
+        if self.gpu is not None:
+            self.gpu.dispose()
+        self.tokensInCache = []
+
+    def sample(self, logits: np.ndarray) -> int:
+        """sample(T=0) (engine.ts:305-309) on the device: first strict maximum over finite
+        logits; raises when none is finite."""
+        buf = self.gpu.upload(np.asarray(logits, np.float32), "sample logits")
+        try:
+            return self.gpu.argmax(buf, int(np.asarray(logits).size))
+        finally:
+            self.gpu.destroy(buf)
