@@ -102,6 +102,17 @@ int wgd_done(wgd_context *ctx);
 int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *x,
                wgd_buffer *y, uint32_t cols, uint32_t rows, uint32_t stride, uint32_t row_base,
                uint32_t input_offset, uint32_t batch);
+/* The decode matvec split in its two steps, for hosts that drive single ops:
+ * wgd_quantize turns an f32 activation row of `cols` elements into the quantized form the
+ * integer matvec reads (buffer of wgd_quantized_bytes(cols)), optionally as RMSNorm(x) * w
+ * (normShader, shaders.ts:55-68, with w = norm_weight, NULL for none); wgd_matvec then
+ * computes y[row_base + r] = sum_c deq(W)[r][c] x[c] for weights uploaded with
+ * wgd_upload_weights (Q4_K, Q6_K, Q8_0). wgd_matmul with batch 1 runs exactly these two. */
+uint64_t wgd_quantized_bytes(uint32_t cols);
+int wgd_quantize(wgd_context *ctx, const wgd_buffer *x, uint32_t cols, const wgd_buffer *norm_weight,
+                 float epsilon, wgd_buffer *qx);
+int wgd_matvec(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *qx, wgd_buffer *y,
+               uint32_t cols, uint32_t rows, uint32_t row_base);
 /* decodeWeight (src/core/quant.ts:6-29) for `count` consecutive elements: out[i] =
  * deq(W)[i] rounded once to f32, bit-identical to the reference's decode. */
 int wgd_dequant(wgd_context *ctx, int32_t type, const wgd_buffer *w, wgd_buffer *out,

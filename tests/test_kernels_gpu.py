@@ -296,3 +296,24 @@ def test_bounds_checks_reject_overruns(gpu):
         gpu.matmul(Q4_K, w, x, y, 256, 1, 1, 1, 0, 1)  # rowBase 1 writes past y
     for b in (w, x, y):
         gpu.destroy(b)
+
+
+# ---------------------------------------------------------------- quantized activation + matvec entries
+@pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 512, 4096), (Q6_K, 256, 5376), (Q8_0, 128, 1024)])
+def test_quantize_with_rms_norm_then_matvec(gpu, type_, rows, cols):
+    """wgd_quantize(x, norm w) + wgd_matvec == W @ (x * rsqrt(mean(x^2) + eps) * w)."""
+    rng = np.random.default_rng(rows)
+    gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+    w = gen(rng, rows * cols // QUANTS[type_]["block"])
+    x = (rng.standard_normal(cols) * 3).astype(np.float32)
+    nw = (1 + rng.uniform(-0.1, 0.1, cols)).astype(np.float32)
+    xn = orc.norm(x, nw, 1e-6).astype(np.float32)
+    want = orc.matmul(type_, w, xn, cols, rows, rows, 0, 0, 1)
+    wb = gpu.upload_weights(type_, cols, rows, w)
+    xb, nb, yb = gpu.upload(x, "x"), gpu.upload(nw, "norm"), gpu.buffer((rows + 3) * 4, "y")
+    qb = gpu.quantized_buffer(cols)
+    gpu.quantize(xb, cols, qb, nb, 1e-6)
+    gpu.matvec(type_, wb, qb, yb, cols, rows, 3)
+    near(gpu.read_f32(yb, rows + 3)[3:], want, 1e-4, f"normed matvec {type_}")
+    for b in (wb, xb, nb, yb, qb):
+        gpu.destroy(b)

@@ -211,7 +211,11 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
   a.nsplit = nsplit;
   size_t lds = sizeof(float) * ((size_t)a.T * (in.hd + 1) + (size_t)a.T * in.hd + (size_t)a.R * in.hd +
                                 (size_t)a.R * a.T + 3 * a.R);
-  if (lds > 65536) (void)hipFuncSetAttribute((const void *)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  static bool big_lds = false;
+  if (lds > 65536 && !big_lds) {
+    (void)hipFuncSetAttribute((const void *)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    big_lds = true;
+  }
   hipLaunchKernelGGL(k_attention, dim3(in.kv_heads, qblocks, nsplit), dim3(256), lds, s, a);
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {

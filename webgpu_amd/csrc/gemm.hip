@@ -62,6 +62,24 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
     }
     return;
   }
+  if (a.type == Q4_K && a.layout == LAYOUT_PLANAR) {
+    Q4Planes p = q4_planes(a.nbt);
+    uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
+    uint32_t j = k & 255, s = j >> 5, l0 = j & 31;
+    uint4 h = *(const uint4 *)(a.w + p.hdr + bi * 16);
+    uint2 qv = *(const uint2 *)(a.w + p.qs + bi * 128 + (s >> 1) * 32 + l0);
+    uint32_t A = h.y, B = h.z, C = h.w, sh = 8 * (s & 3), sc, m;
+    if (s < 4) { sc = (A >> sh) & 63u; m = (B >> sh) & 63u; }
+    else { sc = ((C >> sh) & 15u) | (((A >> sh) >> 6 & 3u) << 4); m = ((C >> sh) >> 4 & 15u) | (((B >> sh) >> 6 & 3u) << 4); }
+    float dsc = half_bits(h.x & 0xFFFFu) * (float)sc, dmm = half_bits(h.x >> 16) * (float)m;
+    uint32_t sq = 4 * (s & 1);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t byte = ((i < 4 ? qv.x : qv.y) >> (8 * (i & 3))) & 0xFFu;
+      o[i] = dsc * (float)((byte >> sq) & 15u) - dmm;
+    }
+    return;
+  }
   if (a.type == Q6_K && a.layout == LAYOUT_PLANAR) {
     Q6Planes p = q6_planes(a.nbt);
     uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);

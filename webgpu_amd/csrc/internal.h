@@ -40,6 +40,8 @@ struct Matrix {
 };
 
 // Planar plane offsets for a matrix of nb blocks.
+struct Q4Planes { uint64_t qs, hdr; };
+__host__ __device__ inline Q4Planes q4_planes(uint64_t nb) { return {0, nb * 128}; }
 struct Q6Planes { uint64_t ql, qh, sc, d; };
 __host__ __device__ inline Q6Planes q6_planes(uint64_t nb) { return {0, nb * 128, nb * 192, nb * 208}; }
 struct Q8Planes { uint64_t qs, d; };
@@ -50,25 +52,15 @@ hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *d
 bool has_planar(int type);
 
 // ---------------------------------------------------------------- launchers
-// Fused-norm hook for matvec prologues: when norm_w is non-null the activation row is
-// replaced by x * inverseSqrt(mean(x^2) + eps) * norm_w before the product (the
-// normShader of shaders.ts:55-68 folded into the consumer).
-struct NormIn { const float *w = nullptr; float eps = 0.f; };
 
-// y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]
+// y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]: the
+// generic kernel for small batches of GGUF-layout weights, else the MFMA dequant-GEMM.
 hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                  uint32_t row_base, uint32_t input_offset, uint32_t batch, NormIn norm = {});
-// Batch-1 fast path with a residual epilogue: y[r] += sum_c W[r][c] x[c].
-hipError_t matmul_add(hipStream_t s, const Matrix &w, const float *x, float *y);
+                  uint32_t row_base, uint32_t input_offset, uint32_t batch);
 hipError_t matmul_generic(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
                           uint32_t row_base, uint32_t input_offset, uint32_t batch);
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
                 uint32_t row_base, uint32_t input_offset, uint32_t batch);
-// Two matrices with identical shape applied to the same (normalised) input, combined
-// by the gated activation: y = act(Wg x) * (Wu x). act 0 = SiLU, 1 = GELU-tanh.
-hipError_t matvec_glu(hipStream_t s, const Matrix &wg, const Matrix &wu, const float *x, float *y,
-                      int act, NormIn norm);
-bool fast_matvec_ok(const Matrix &w);
 
 hipError_t dequant(hipStream_t s, int type, const uint8_t *w, float *out, uint64_t count);
 hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *ids, float *out,

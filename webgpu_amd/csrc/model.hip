@@ -12,11 +12,14 @@
 //     layer, engine.ts:152-174, and reads logits back for a CPU argmax, :179, :291).
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
 
 #include "internal.h"
+#include "matvec.h"
 #include "model.h"
 
 using namespace wgd;
@@ -60,6 +63,11 @@ struct wgd_model {
   int32_t *tokens = nullptr;    // decode output ring, one per position
   int32_t *argmax_buf = nullptr;
   float *att_part = nullptr; uint64_t att_part_floats = 0;
+  bool use_graph = true;         // WGD_GRAPH=0 disables capture (profilers, debugging)
+  // Quantized-activation decode path (every matrix Q4_K, Q6_K or Q8_0): activation buffers
+  // in the QX format.
+  bool qpath = false;
+  void *qx_attn = nullptr, *qx_ffn = nullptr, *qx_o = nullptr, *qx_down = nullptr, *qx_head = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   std::vector<void *> owned;
@@ -118,8 +126,9 @@ hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, cons
   return attention(s, a);
 }
 
-// Prompt chunk: n tokens already gathered into m->hidden.
-hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start) {
+// n tokens already gathered into m->hidden (a prompt chunk, or one decode token on the
+// generic path with its position in device memory).
+hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_t *start_dev = nullptr) {
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
   const uint32_t H = c.hidden, qd = c.heads * c.head_dim, kd = c.kv_heads * c.head_dim, F = c.intermediate;
@@ -132,7 +141,7 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start) {
     WGD_HIP(bias(s, m->k, L.bk, n, kd));
     WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, n));
     WGD_HIP(bias(s, m->v, L.bv, n, kd));
-    WGD_HIP(attention_block(m, l, n, start, nullptr));
+    WGD_HIP(attention_block(m, l, n, start, start_dev));
     WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, n));
     WGD_HIP(bias(s, m->proj, L.bo, n, H));
     if (is_gemma(m)) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, n));
@@ -154,19 +163,14 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start) {
   return hipSuccess;
 }
 
-// Logits of row `row` of m->hidden: output norm folded into the head matvec.
+// Logits of row `row` of m->hidden (output norm, head matvec, greedy argmax) for the
+// batched and generic paths.
 hipError_t head(wgd_model *m, uint32_t row) {
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
   const Matrix &W = m->have_output && !c.tied_output ? m->output : m->embd;
-  const float *x = m->hidden + (uint64_t)row * c.hidden;
-  if (fast_matvec_ok(W)) {
-    NormIn nin; nin.w = m->out_norm; nin.eps = c.epsilon;
-    WGD_HIP(matmul(s, W, x, m->logits, c.vocab, 0, 0, 1, nin));
-  } else {
-    WGD_HIP(norm(s, x, m->out_norm, m->normed, c.hidden, c.epsilon, 1));
-    WGD_HIP(matmul(s, W, m->normed, m->logits, c.vocab, 0, 0, 1));
-  }
+  WGD_HIP(norm(s, m->hidden + (uint64_t)row * c.hidden, m->out_norm, m->normed, c.hidden, c.epsilon, 1));
+  WGD_HIP(matmul(s, W, m->normed, m->logits, c.vocab, 0, 0, 1));
   return argmax(s, m->logits, c.vocab, m->argmax_buf);
 }
 
@@ -181,62 +185,81 @@ __global__ void k_advance(StepState *st, const int32_t *arg, int32_t *tokens, ui
   st->step += 1;
 }
 
-// One decode step with n = 1 reading position and token id from device state.
-hipError_t decode_step(wgd_model *m, bool advance) {
+QXView qv(void *p, uint32_t K) { return qx_const(qx_view(p, K)); }
+
+// Decode step on quantized activations: every matvec reads a QX vector produced by the
+// previous kernel; the O and down projections add into the residual stream and re-quantize
+// the next RMSNorm's input (x * w, with the norm's 1/rms reduced across the row tiles).
+hipError_t decode_step_q(wgd_model *m, bool advance) {
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
   const uint32_t H = c.hidden, qd = c.heads * c.head_dim, kd = c.kv_heads * c.head_dim, F = c.intermediate;
   const int32_t *pos = &m->state->pos;
+  const bool gemma = is_gemma(m);
   WGD_HIP(embed_matrix(s, m->embd, &m->state->token, m->hidden, 1, c.embed_scale));
+  WGD_HIP(quantize(s, m->hidden, H, m->L[0].attn_norm, c.epsilon, qx_view(m->qx_attn, H)));
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
-    NormIn an; an.w = L.attn_norm; an.eps = c.epsilon;
-    const bool fq = fast_matvec_ok(L.q) && fast_matvec_ok(L.k) && fast_matvec_ok(L.v);
-    if (fq) {
-      WGD_HIP(matmul(s, L.q, m->hidden, m->q, qd, 0, 0, 1, an));
-      WGD_HIP(matmul(s, L.k, m->hidden, m->k, kd, 0, 0, 1, an));
-      WGD_HIP(matmul(s, L.v, m->hidden, m->v, kd, 0, 0, 1, an));
-    } else {
-      WGD_HIP(norm(s, m->hidden, L.attn_norm, m->normed, H, c.epsilon, 1));
-      WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, 1));
-      WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, 1));
-      WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, 1));
-    }
+    const QXView xa = qv(m->qx_attn, H);
+    WGD_HIP(mv(s, L.q, nullptr, xa, m->q, 0, MV_STORE));
+    WGD_HIP(mv(s, L.k, nullptr, xa, m->k, 0, MV_STORE));
+    WGD_HIP(mv(s, L.v, nullptr, xa, m->v, 0, MV_STORE));
     WGD_HIP(bias(s, m->q, L.bq, 1, qd));
     WGD_HIP(bias(s, m->k, L.bk, 1, kd));
     WGD_HIP(bias(s, m->v, L.bv, 1, kd));
     WGD_HIP(attention_block(m, l, 1, 0, pos));
-    if (!is_gemma(m) && !L.bo && fast_matvec_ok(L.o)) {
-      WGD_HIP(matmul_add(s, L.o, m->att, m->hidden));
+    WGD_HIP(quantize(s, m->att, qd, nullptr, 0.f, qx_view(m->qx_o, qd)));
+    MVOut to_ffn;
+    to_ffn.q = qx_view(m->qx_ffn, H); to_ffn.norm_w = L.ffn_norm; to_ffn.eps = c.epsilon;
+    if (!gemma && !L.bo) {
+      WGD_HIP(mv(s, L.o, nullptr, qv(m->qx_o, qd), m->hidden, 0, MV_ADD, &to_ffn));
     } else {
-      WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, 1));
+      WGD_HIP(mv(s, L.o, nullptr, qv(m->qx_o, qd), m->proj, 0, MV_STORE));
       WGD_HIP(bias(s, m->proj, L.bo, 1, H));
-      if (is_gemma(m)) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, 1));
+      if (gemma) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, 1));
       else WGD_HIP(add(s, m->proj, m->hidden, H));
+      WGD_HIP(quantize(s, m->hidden, H, L.ffn_norm, c.epsilon, to_ffn.q));
     }
-    NormIn fn; fn.w = L.ffn_norm; fn.eps = c.epsilon;
-    float *ffn_in = m->prod;
-    if (c.ffn_gate && fast_matvec_ok(L.gate) && L.gate.type == L.up.type && L.gate.layout == L.up.layout) {
-      WGD_HIP(matvec_glu(s, L.gate, L.up, m->hidden, m->prod, c.gelu, fn));
+    MVOut to_down;
+    to_down.q = qx_view(m->qx_down, F);
+    const QXView xf = qv(m->qx_ffn, H);
+    if (c.ffn_gate) {
+      WGD_HIP(mv(s, L.gate, &L.up, xf, m->prod, 0, c.gelu ? MV_GELU : MV_SILU, &to_down));
     } else {
-      WGD_HIP(norm(s, m->hidden, L.ffn_norm, m->normed, H, c.epsilon, 1));
-      WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, 1));
-      if (c.ffn_gate) {
-        WGD_HIP(matmul(s, L.gate, m->normed, m->gate, F, 0, 0, 1));
-        WGD_HIP(glu(s, m->gate, m->up, m->prod, F, c.gelu));
-      } else {
-        WGD_HIP(activate(s, m->up, F));
-        ffn_in = m->up;
-      }
+      WGD_HIP(mv(s, L.up, nullptr, xf, m->up, 0, MV_STORE));
+      WGD_HIP(activate(s, m->up, F));
+      WGD_HIP(quantize(s, m->up, F, nullptr, 0.f, to_down.q));
     }
-    if (!is_gemma(m) && fast_matvec_ok(L.down)) {
-      WGD_HIP(matmul_add(s, L.down, ffn_in, m->hidden));
+    const bool last = l + 1 == c.layers;
+    MVOut next;
+    next.q = qx_view(last ? m->qx_head : m->qx_attn, H);
+    next.norm_w = last ? m->out_norm : m->L[l + 1].attn_norm;
+    next.eps = c.epsilon;
+    if (!gemma) {
+      WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->hidden, 0, MV_ADD, &next));
     } else {
-      WGD_HIP(matmul(s, L.down, ffn_in, m->down, H, 0, 0, 1));
-      if (is_gemma(m)) WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, 1));
-      else WGD_HIP(add(s, m->down, m->hidden, H));
+      WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->down, 0, MV_STORE));
+      WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, 1));
+      WGD_HIP(quantize(s, m->hidden, H, next.norm_w, c.epsilon, next.q));
     }
   }
+  const Matrix &W = m->have_output && !c.tied_output ? m->output : m->embd;
+  WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H), m->logits, 0, MV_STORE));
+  WGD_HIP(argmax(s, m->logits, c.vocab, m->argmax_buf));
+  if (advance) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, m->state, (const int32_t *)m->argmax_buf, m->tokens,
+                       (uint32_t)m->c.context);
+    WGD_HIP(hipGetLastError());
+  }
+  return hipSuccess;
+}
+
+// One decode step with n = 1 for models whose matrices the quantized matvec does not read
+// (F32, F16, Q4_0, Q5_K): the batched kernels with the position read from device state.
+hipError_t decode_step_generic(wgd_model *m, bool advance) {
+  hipStream_t s = m->ctx->stream;
+  WGD_HIP(embed_matrix(s, m->embd, &m->state->token, m->hidden, 1, m->c.embed_scale));
+  WGD_HIP(layers_batched(m, 1, 0, &m->state->pos));
   WGD_HIP(head(m, 0));
   if (advance) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, m->state, (const int32_t *)m->argmax_buf, m->tokens,
@@ -244,6 +267,10 @@ hipError_t decode_step(wgd_model *m, bool advance) {
     WGD_HIP(hipGetLastError());
   }
   return hipSuccess;
+}
+
+hipError_t decode_step(wgd_model *m, bool advance) {
+  return m->qpath ? decode_step_q(m, advance) : decode_step_generic(m, advance);
 }
 
 int validate_ids(wgd_model *m, const int32_t *ids, int32_t n) {
@@ -289,6 +316,8 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
   m->L.resize(c.layers);
   m->seen.assign(c.layers, 0);
   ctx->models.insert(m);
+  const char *g = getenv("WGD_GRAPH");
+  m->use_graph = !(g && g[0] == '0');
   const uint64_t B = c.batch, H = c.hidden, qd = (uint64_t)c.heads * c.head_dim, kd = (uint64_t)c.kv_heads * c.head_dim,
                  F = c.intermediate;
   int rc = WGD_OK;
@@ -458,6 +487,27 @@ int wgd_model_ready(wgd_model *m) {
       }
   }
   if (rc) return rc;
+  // The quantized decode path needs every matrix in a type the integer matvec reads.
+  const Matrix &head_w = m->have_output && !c.tied_output ? m->output : m->embd;
+  bool q = mv_supported(head_w);
+  for (int l = 0; q && l < c.layers; l++) {
+    const Layer &L = m->L[l];
+    q = mv_supported(L.q) && mv_supported(L.k) && mv_supported(L.v) && mv_supported(L.o) &&
+        mv_supported(L.up) && mv_supported(L.down) &&
+        (!c.ffn_gate || (mv_supported(L.gate) && L.gate.type == L.up.type && L.gate.layout == L.up.layout));
+  }
+  const char *env = getenv("WGD_QMATVEC");
+  if (env && env[0] == '0') q = false;
+  if (q) {
+    const uint32_t H = c.hidden, qd = c.heads * c.head_dim, F = c.intermediate;
+    rc = alloc(m, qx_bytes(H), "qx attn", &m->qx_attn);
+    rc = rc ? rc : alloc(m, qx_bytes(H), "qx ffn", &m->qx_ffn);
+    rc = rc ? rc : alloc(m, qx_bytes(qd), "qx o", &m->qx_o);
+    rc = rc ? rc : alloc(m, qx_bytes(F), "qx down", &m->qx_down);
+    rc = rc ? rc : alloc(m, qx_bytes(H), "qx head", &m->qx_head);
+    if (rc) return rc;
+    m->qpath = true;
+  }
   m->ready = true;
   return ctx_sync(ctx, "model upload");
 }
@@ -512,7 +562,11 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count, 
   StepState st = {start, token, 0, 0};
   rc = ctx_check(ctx, hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s), "decode");
   if (rc) return rc;
-  if (!m->exec) {
+  if (!m->use_graph) {
+    // Eager launches (WGD_GRAPH=0): same kernels, one host launch each; used under tracers.
+    for (int32_t i = 0; i < count && !rc; i++) rc = ctx_check(ctx, decode_step(m, true), "decode");
+    if (rc) return rc;
+  } else if (!m->exec) {
     // Run one step eagerly first: it validates every launch outside capture.
     rc = ctx_check(ctx, decode_step(m, true), "decode");
     if (!rc) rc = ctx_sync(ctx, "GPU fault during decode");

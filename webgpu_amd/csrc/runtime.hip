@@ -10,6 +10,7 @@
 #include <string>
 
 #include "internal.h"
+#include "matvec.h"
 #include "model.h"
 
 using namespace wgd;
@@ -259,7 +260,52 @@ int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
       return fail(ctx, WGD_E_INVALID, "matmul: weights %s were uploaded as type %d, %ux%u", w->label.c_str(), w->type, w->cols, w->rows);
     m.layout = w->layout;
   }
+  if (batch == 1 && mv_supported(m)) {
+    // Decode path: quantize the activation row, then the split-K integer-dot matvec.
+    auto grow = [&](void **p, uint64_t *have, uint64_t need, const char *label) -> int {
+      if (need <= *have) return WGD_OK;
+      ctx_free(ctx, *p);
+      *p = nullptr; *have = 0;
+      int rc = ctx_alloc(ctx, need, label, p);  // zero-filled: the counters start at zero
+      if (!rc) *have = need;
+      return rc;
+    };
+    int rc = grow(&ctx->mv_qx, &ctx->mv_qx_bytes, qx_bytes(cols), "matvec activation");
+    if (rc) return rc;
+    QXOut q = qx_view(ctx->mv_qx, cols);
+    rc = ctx_check(ctx, quantize(ctx->stream, (const float *)x->ptr + (uint64_t)input_offset * cols, cols, nullptr, 0.f, q), "matmul");
+    if (rc) return rc;
+    return ctx_check(ctx, mv(ctx->stream, m, nullptr, qx_const(q), (float *)y->ptr, row_base, MV_STORE), "matmul");
+  }
   return ctx_check(ctx, matmul(ctx->stream, m, (const float *)x->ptr, (float *)y->ptr, stride, row_base, input_offset, batch), "matmul");
+}
+
+uint64_t wgd_quantized_bytes(uint32_t cols) { return qx_bytes(cols); }
+
+int wgd_quantize(wgd_context *ctx, const wgd_buffer *x, uint32_t cols, const wgd_buffer *norm_weight, float epsilon,
+                 wgd_buffer *qx) {
+  NEED_CTX(ctx); NEED_BUF(ctx, x, "quantize"); NEED_BUF(ctx, qx, "quantize");
+  if (!cols || (cols + 255) / 256 > QX_MAX_TILES) return fail(ctx, WGD_E_INVALID, "quantize: %u columns", cols);
+  NEED_FIT(ctx, x, (uint64_t)cols * 4, "quantize input");
+  NEED_FIT(ctx, qx, qx_bytes(cols), "quantized activation");
+  if (norm_weight) { NEED_BUF(ctx, norm_weight, "quantize"); NEED_FIT(ctx, norm_weight, (uint64_t)cols * 4, "norm weight"); }
+  return ctx_check(ctx, quantize(ctx->stream, (const float *)x->ptr, cols, norm_weight ? (const float *)norm_weight->ptr : nullptr,
+                                 epsilon, qx_view(qx->ptr, cols)), "quantize");
+}
+
+int wgd_matvec(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *qx, wgd_buffer *y, uint32_t cols,
+               uint32_t rows, uint32_t row_base) {
+  NEED_CTX(ctx); NEED_BUF(ctx, w, "matvec"); NEED_BUF(ctx, qx, "matvec"); NEED_BUF(ctx, y, "matvec");
+  if (!known_type(type) || !cols || cols % block_size(type)) return fail(ctx, WGD_E_INVALID, "matvec: type %d, %u columns", type, cols);
+  if (!rows) return WGD_OK;
+  NEED_FIT(ctx, w, (uint64_t)rows * row_bytes(type, cols), "matvec weights");
+  NEED_FIT(ctx, qx, qx_bytes(cols), "quantized activation");
+  NEED_FIT(ctx, y, ((uint64_t)row_base + rows) * 4, "matvec output");
+  Matrix m; m.data = (const uint8_t *)w->ptr; m.type = type; m.layout = w->layout; m.cols = cols; m.rows = rows;
+  if (w->layout != LAYOUT_GGUF && (w->type != type || w->cols != cols || w->rows != rows))
+    return fail(ctx, WGD_E_INVALID, "matvec: weights %s were uploaded as type %d, %ux%u", w->label.c_str(), w->type, w->cols, w->rows);
+  if (!mv_supported(m)) return fail(ctx, WGD_E_INVALID, "matvec: type %d in this layout has no quantized matvec (upload with wgd_upload_weights)", type);
+  return ctx_check(ctx, mv(ctx->stream, m, nullptr, qx_const(qx_view(qx->ptr, cols)), (float *)y->ptr, row_base, MV_STORE), "matvec");
 }
 
 int wgd_dequant(wgd_context *ctx, int32_t type, const wgd_buffer *w, wgd_buffer *out, uint64_t count) {

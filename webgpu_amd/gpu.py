@@ -40,6 +40,9 @@ SIGNATURES = {
     "wgd_done": (C.c_int, [_P]),
     "wgd_matmul": (C.c_int, [_P, _I32, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32]),
     "wgd_dequant": (C.c_int, [_P, _I32, _P, _P, _U64]),
+    "wgd_quantized_bytes": (_U64, [_U32]),
+    "wgd_quantize": (C.c_int, [_P, _P, _U32, _P, _F, _P]),
+    "wgd_matvec": (C.c_int, [_P, _I32, _P, _P, _P, _U32, _U32, _U32]),
     "wgd_norm": (C.c_int, [_P, _P, _P, _P, _U32, _F, _U32]),
     "wgd_rope_norm": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _F, _F, _F, _U32, _U32]),
     "wgd_rope_neox": (C.c_int, [_P, _P, _U32, _U32, _U32, _F, _F, _U32, _U32]),
@@ -201,6 +204,16 @@ class Compute:
                row_base: int, input_offset: int, batch: int = 1) -> None:
         self.check(lib().wgd_matmul(self.ctx, type_, w.ptr, x.ptr, y.ptr, cols, rows, stride, row_base,
                                     input_offset, batch))
+
+    def quantized_buffer(self, cols: int, label: str = "quantized activation") -> Buffer:
+        return self.buffer(lib().wgd_quantized_bytes(cols), label)
+
+    def quantize(self, x: Buffer, cols: int, qx: Buffer, norm_weight: Optional[Buffer] = None,
+                 epsilon: float = 0.0) -> None:
+        self.check(lib().wgd_quantize(self.ctx, x.ptr, cols, norm_weight.ptr if norm_weight else None, epsilon, qx.ptr))
+
+    def matvec(self, type_: int, w: Buffer, qx: Buffer, y: Buffer, cols: int, rows: int, row_base: int = 0) -> None:
+        self.check(lib().wgd_matvec(self.ctx, type_, w.ptr, qx.ptr, y.ptr, cols, rows, row_base))
 
     def dequant(self, type_: int, w: Buffer, out: Buffer, count: int) -> None:
         self.check(lib().wgd_dequant(self.ctx, type_, w.ptr, out.ptr, count))
