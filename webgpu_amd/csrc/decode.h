@@ -57,6 +57,23 @@ __device__ __forceinline__ float deq_elem(int type, const uint8_t *b, uint64_t i
   return __uint_as_float(0x7fc00000u);
 }
 
+// ------------------------------------------------------------------ planar chunk layouts
+// (written by repack_planar, quant.hip). Chunk ci = block * 8 + sub-block holds 32 elements.
+
+// Q4_K quant of element e (0..31) of chunk ci: byte e % 16, nibble e / 16.
+__device__ __forceinline__ uint32_t q4_quant(const uint8_t *w, uint64_t ci, uint32_t e) {
+  return (w[ci * 16 + (e & 15)] >> (4 * (e >> 4))) & 15u;
+}
+// Q6_K 6-bit quant of element e (0..31) of chunk ci: low nibble as Q4_K in the ql plane; the
+// high 2 bits in qh byte 4 * ((e % 16) / 8) + e % 4 at bit 4 * ((e % 8) / 4) + 2 * (e / 16).
+__device__ __forceinline__ uint32_t q6_quant(const uint8_t *w, uint64_t nbt, uint64_t ci, uint32_t e) {
+  const Q6Planes p = q6_planes(nbt);
+  const uint32_t lo = (w[p.ql + ci * 16 + (e & 15)] >> (4 * (e >> 4))) & 15u;
+  const uint32_t r = e & 15;
+  const uint32_t hi = (w[p.qh + ci * 8 + 4 * (r >> 3) + (r & 3)] >> (4 * ((r & 7) >> 2) + 2 * (e >> 4))) & 3u;
+  return lo | (hi << 4);
+}
+
 // ------------------------------------------------------------------ wave reduction
 
 __device__ __forceinline__ float wave_sum(float v) {

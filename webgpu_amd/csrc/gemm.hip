@@ -64,15 +64,16 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
   }
   if (a.type == Q4_K && a.layout == LAYOUT_PLANAR) {
     Q4Planes p = q4_planes(a.nbt);
-    uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
-    uint32_t j = k & 255, s = j >> 5, l0 = j & 31;
+    const uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
+    const uint32_t j = k & 255, s = j >> 5, e0 = j & 31;
     uint4 h = *(const uint4 *)(a.w + p.hdr + bi * 16);
-    uint2 qv = *(const uint2 *)(a.w + p.qs + bi * 128 + (s >> 1) * 32 + l0);
+    // chunk s, bytes e0 % 16 .. +8, nibble e0 / 16
+    uint2 qv = *(const uint2 *)(a.w + p.qs + (bi * 8 + s) * 16 + (e0 & 15));
     uint32_t A = h.y, B = h.z, C = h.w, sh = 8 * (s & 3), sc, m;
     if (s < 4) { sc = (A >> sh) & 63u; m = (B >> sh) & 63u; }
     else { sc = ((C >> sh) & 15u) | (((A >> sh) >> 6 & 3u) << 4); m = ((C >> sh) >> 4 & 15u) | (((B >> sh) >> 6 & 3u) << 4); }
     float dsc = half_bits(h.x & 0xFFFFu) * (float)sc, dmm = half_bits(h.x >> 16) * (float)m;
-    uint32_t sq = 4 * (s & 1);
+    uint32_t sq = 4 * (e0 >> 4);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       uint32_t byte = ((i < 4 ? qv.x : qv.y) >> (8 * (i & 3))) & 0xFFu;
@@ -82,17 +83,20 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
   }
   if (a.type == Q6_K && a.layout == LAYOUT_PLANAR) {
     Q6Planes p = q6_planes(a.nbt);
-    uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
-    uint32_t j = k & 255, seg = j >> 7, qtr = (j & 127) >> 5, ln = j & 31;
-    uint2 lo = *(const uint2 *)(a.w + p.ql + bi * 128 + seg * 64 + (qtr & 1) * 32 + ln);
-    uint2 hi = *(const uint2 *)(a.w + p.qh + bi * 64 + seg * 32 + ln);
-    float sc = (float)(int8_t)a.w[p.sc + bi * 16 + seg * 8 + qtr * 2 + ln / 16];
+    const uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
+    const uint32_t j = k & 255, s = j >> 5, e0 = j & 31, h = e0 >> 4;
+    const uint64_t ci = bi * 8 + s;
+    uint2 lo = *(const uint2 *)(a.w + p.ql + ci * 16 + (e0 & 15));
+    // high bits of elements e0 .. e0+7: qh dword (e0 % 16) / 8, byte i % 4, bit 4 * (i / 4) + 2h
+    uint32_t hq = *(const uint32_t *)(a.w + p.qh + ci * 8 + 4 * ((e0 & 15) >> 3));
+    float sc = (float)(int8_t)a.w[p.sc + ci * 2 + h];
     float d = half_bits(*(const uint16_t *)(a.w + p.d + bi * 2)) * sc;
-    uint32_t ls = 4 * (qtr >> 1), hs = 2 * qtr;
+    uint32_t ls = 4 * h;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      uint32_t lb = ((i < 4 ? lo.x : lo.y) >> (8 * (i & 3))) & 0xFFu, hb = ((i < 4 ? hi.x : hi.y) >> (8 * (i & 3))) & 0xFFu;
-      o[i] = d * (float)((int)(((lb >> ls) & 15u) | (((hb >> hs) & 3u) << 4)) - 32);
+      uint32_t lb = ((i < 4 ? lo.x : lo.y) >> (8 * (i & 3))) & 0xFFu;
+      uint32_t hb = (hq >> (8 * (i & 3) + 4 * (i >> 2) + 2 * h)) & 3u;
+      o[i] = d * (float)((int)(((lb >> ls) & 15u) | (hb << 4)) - 32);
     }
     return;
   }

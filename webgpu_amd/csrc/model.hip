@@ -185,66 +185,79 @@ __global__ void k_advance(StepState *st, const int32_t *arg, int32_t *tokens, ui
   st->step += 1;
 }
 
-QXView qv(void *p, uint32_t K) { return qx_const(qx_view(p, K)); }
+QXView qv(void *p, uint32_t K, bool normed = false, float eps = 0.f) { return qx_const(qx_view(p, K), K, normed, eps); }
+
+// Matvecs of several matrices that read the same activation, one launch per weight type.
+hipError_t mv_group(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x) {
+  bool done[MV_MAX_SEGS] = {};
+  for (uint32_t i = 0; i < n; i++) {
+    if (done[i]) continue;
+    MVTarget grp[MV_MAX_SEGS];
+    uint32_t k = 0;
+    for (uint32_t j = i; j < n; j++)
+      if (!done[j] && t[j].w->type == t[i].w->type) { grp[k++] = t[j]; done[j] = true; }
+    WGD_HIP(mv(s, grp, k, x, MV_STORE));
+  }
+  return hipSuccess;
+}
 
 // Decode step on quantized activations: every matvec reads a QX vector produced by the
 // previous kernel; the O and down projections add into the residual stream and re-quantize
-// the next RMSNorm's input (x * w, with the norm's 1/rms reduced across the row tiles).
+// the next RMSNorm's input (x * w; the consumer applies 1/rms from the stored squares).
 hipError_t decode_step_q(wgd_model *m, bool advance) {
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
-  const uint32_t H = c.hidden, qd = c.heads * c.head_dim, kd = c.kv_heads * c.head_dim, F = c.intermediate;
+  const uint32_t H = c.hidden, qd = c.heads * c.head_dim, F = c.intermediate;
   const int32_t *pos = &m->state->pos;
   const bool gemma = is_gemma(m);
   WGD_HIP(embed_matrix(s, m->embd, &m->state->token, m->hidden, 1, c.embed_scale));
-  WGD_HIP(quantize(s, m->hidden, H, m->L[0].attn_norm, c.epsilon, qx_view(m->qx_attn, H)));
+  WGD_HIP(quantize(s, m->hidden, H, m->L[0].attn_norm, qx_view(m->qx_attn, H)));
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
-    const QXView xa = qv(m->qx_attn, H);
-    WGD_HIP(mv(s, L.q, nullptr, xa, m->q, 0, MV_STORE));
-    WGD_HIP(mv(s, L.k, nullptr, xa, m->k, 0, MV_STORE));
-    WGD_HIP(mv(s, L.v, nullptr, xa, m->v, 0, MV_STORE));
-    WGD_HIP(bias(s, m->q, L.bq, 1, qd));
-    WGD_HIP(bias(s, m->k, L.bk, 1, kd));
-    WGD_HIP(bias(s, m->v, L.bv, 1, kd));
+    MVTarget qkv[3];
+    qkv[0].w = &L.q; qkv[0].y = m->q; qkv[0].bias = L.bq;
+    qkv[1].w = &L.k; qkv[1].y = m->k; qkv[1].bias = L.bk;
+    qkv[2].w = &L.v; qkv[2].y = m->v; qkv[2].bias = L.bv;
+    WGD_HIP(mv_group(s, qkv, 3, qv(m->qx_attn, H, true, c.epsilon)));
     WGD_HIP(attention_block(m, l, 1, 0, pos));
-    WGD_HIP(quantize(s, m->att, qd, nullptr, 0.f, qx_view(m->qx_o, qd)));
+    WGD_HIP(quantize(s, m->att, qd, nullptr, qx_view(m->qx_o, qd)));
     MVOut to_ffn;
-    to_ffn.q = qx_view(m->qx_ffn, H); to_ffn.norm_w = L.ffn_norm; to_ffn.eps = c.epsilon;
-    if (!gemma && !L.bo) {
-      WGD_HIP(mv(s, L.o, nullptr, qv(m->qx_o, qd), m->hidden, 0, MV_ADD, &to_ffn));
+    to_ffn.q = qx_view(m->qx_ffn, H); to_ffn.norm_w = L.ffn_norm;
+    MVTarget o;
+    o.w = &L.o; o.bias = L.bo;
+    if (!gemma) {
+      o.y = m->hidden;
+      WGD_HIP(mv(s, &o, 1, qv(m->qx_o, qd), MV_ADD, &to_ffn));
     } else {
-      WGD_HIP(mv(s, L.o, nullptr, qv(m->qx_o, qd), m->proj, 0, MV_STORE));
-      WGD_HIP(bias(s, m->proj, L.bo, 1, H));
-      if (gemma) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, 1));
-      else WGD_HIP(add(s, m->proj, m->hidden, H));
-      WGD_HIP(quantize(s, m->hidden, H, L.ffn_norm, c.epsilon, to_ffn.q));
+      o.y = m->proj;
+      WGD_HIP(mv(s, &o, 1, qv(m->qx_o, qd), MV_STORE));
+      WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, 1));
+      WGD_HIP(quantize(s, m->hidden, H, L.ffn_norm, to_ffn.q));
     }
     MVOut to_down;
     to_down.q = qx_view(m->qx_down, F);
-    const QXView xf = qv(m->qx_ffn, H);
+    const QXView xf = qv(m->qx_ffn, H, true, c.epsilon);
     if (c.ffn_gate) {
-      WGD_HIP(mv(s, L.gate, &L.up, xf, m->prod, 0, c.gelu ? MV_GELU : MV_SILU, &to_down));
+      WGD_HIP(mv(s, L.gate, &L.up, xf, m->prod, c.gelu ? MV_GELU : MV_SILU, &to_down));
     } else {
-      WGD_HIP(mv(s, L.up, nullptr, xf, m->up, 0, MV_STORE));
+      WGD_HIP(mv(s, L.up, nullptr, xf, m->up, MV_STORE));
       WGD_HIP(activate(s, m->up, F));
-      WGD_HIP(quantize(s, m->up, F, nullptr, 0.f, to_down.q));
+      WGD_HIP(quantize(s, m->up, F, nullptr, to_down.q));
     }
     const bool last = l + 1 == c.layers;
     MVOut next;
     next.q = qx_view(last ? m->qx_head : m->qx_attn, H);
     next.norm_w = last ? m->out_norm : m->L[l + 1].attn_norm;
-    next.eps = c.epsilon;
     if (!gemma) {
-      WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->hidden, 0, MV_ADD, &next));
+      WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->hidden, MV_ADD, &next));
     } else {
-      WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->down, 0, MV_STORE));
+      WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->down, MV_STORE));
       WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, 1));
-      WGD_HIP(quantize(s, m->hidden, H, next.norm_w, c.epsilon, next.q));
+      WGD_HIP(quantize(s, m->hidden, H, next.norm_w, next.q));
     }
   }
   const Matrix &W = m->have_output && !c.tied_output ? m->output : m->embd;
-  WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H), m->logits, 0, MV_STORE));
+  WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H, true, c.epsilon), m->logits, MV_STORE));
   WGD_HIP(argmax(s, m->logits, c.vocab, m->argmax_buf));
   if (advance) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, m->state, (const int32_t *)m->argmax_buf, m->tokens,

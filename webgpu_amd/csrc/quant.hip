@@ -46,28 +46,26 @@ hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *i
   return hipGetLastError();
 }
 
-// Gather from a planar Q6_K / Q8_0 table: element i of `row`, decoded exactly as deq_elem.
+// Gather from a planar table: element i of `row`, decoded exactly as deq_elem.
 __device__ __forceinline__ float deq_planar(int type, const uint8_t *w, uint64_t nbt, uint32_t bpr, uint32_t row, uint32_t i) {
-  uint64_t bi = (uint64_t)row * bpr + i / block_size_dev(type);
+  const uint64_t bi = (uint64_t)row * bpr + i / block_size_dev(type);
   if (type == Q4_K) {
-    // The GGUF element decode over the block re-assembled from its two planes.
-    Q4Planes p = q4_planes(nbt);
-    const uint8_t *h = w + p.hdr + bi * 16, *qs = w + p.qs + bi * 128;
-    uint32_t j = i % 256, s = j / 32, sc, mn;
+    const uint8_t *h = w + q4_planes(nbt).hdr + bi * 16;
+    const uint32_t j = i % 256, s = j / 32, e = j % 32;
+    uint32_t sc, mn;
     if (s < 4) { sc = h[4 + s] & 63u; mn = h[8 + s] & 63u; }
     else { sc = (h[8 + s] & 15u) | ((h[s] >> 6) << 4); mn = (h[8 + s] >> 4) | ((h[4 + s] >> 6) << 4); }
-    uint32_t q = (qs[(j / 64) * 32 + j % 32] >> ((s % 2) * 4)) & 15u;
+    const uint32_t q = q4_quant(w, bi * 8 + s, e);
     return half_bits(h[0] | ((uint32_t)h[1] << 8)) * (float)(sc * q) - half_bits(h[2] | ((uint32_t)h[3] << 8)) * (float)mn;
   }
   if (type == Q6_K) {
-    Q6Planes p = q6_planes(nbt);
-    uint32_t j = i % 256, seg = j / 128, qtr = (j % 128) / 32, ln = j % 32;
-    uint32_t lo = (w[p.ql + bi * 128 + seg * 64 + (qtr % 2) * 32 + ln] >> ((qtr / 2) * 4)) & 15u;
-    uint32_t hi = (w[p.qh + bi * 64 + seg * 32 + ln] >> (qtr * 2)) & 3u;
-    float sc = (float)(int8_t)w[p.sc + bi * 16 + seg * 8 + qtr * 2 + ln / 16];
-    return half_bits(w[p.d + bi * 2] | ((uint32_t)w[p.d + bi * 2 + 1] << 8)) * sc * (float)((int)(lo | (hi << 4)) - 32);
+    const Q6Planes p = q6_planes(nbt);
+    const uint32_t j = i % 256, s = j / 32, e = j % 32;
+    const uint64_t ci = bi * 8 + s;
+    const float sc = (float)(int8_t)w[p.sc + ci * 2 + e / 16];
+    return half_bits(w[p.d + bi * 2] | ((uint32_t)w[p.d + bi * 2 + 1] << 8)) * sc * (float)((int)q6_quant(w, nbt, ci, e) - 32);
   }
-  Q8Planes p = q8_planes(nbt);
+  const Q8Planes p = q8_planes(nbt);
   return half_bits(w[p.d + bi * 2] | ((uint32_t)w[p.d + bi * 2 + 1] << 8)) * (float)(int8_t)w[p.qs + bi * 32 + i % 32];
 }
 
@@ -94,22 +92,47 @@ hipError_t embed_matrix(hipStream_t s, const Matrix &t, const int32_t *ids, floa
 
 bool has_planar(int type) { return type == Q4_K || type == Q6_K || type == Q8_0; }
 
+// One thread per block. Q4_K: chunk j (sub-block j) byte i = q[32j + i] | q[32j + 16 + i] << 4,
+// with q[e] the GGUF quant of element e (byte 16 + 32*(e/64) + e%32, nibble (e%64)/32).
 __global__ void k_repack_q4(const uint8_t *src, uint8_t *dst, uint64_t nb) {
-  Q4Planes p = q4_planes(nb);
-  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nb * 144; i += (uint64_t)gridDim.x * blockDim.x) {
-    uint64_t blk = i / 144; uint32_t o = i % 144; uint8_t v = src[i];
-    if (o < 16) dst[p.hdr + blk * 16 + o] = v; else dst[p.qs + blk * 128 + (o - 16)] = v;
+  const Q4Planes p = q4_planes(nb);
+  for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
+    const uint8_t *b = src + blk * 144;
+    for (int o = 0; o < 16; o++) dst[p.hdr + blk * 16 + o] = b[o];
+    auto q = [&](uint32_t e) -> uint32_t { return (b[16 + 32 * (e / 64) + e % 32] >> (4 * ((e % 64) / 32))) & 15u; };
+    for (uint32_t j = 0; j < 8; j++)
+      for (uint32_t i = 0; i < 16; i++) dst[p.qs + blk * 128 + 16 * j + i] = (uint8_t)(q(32 * j + i) | (q(32 * j + 16 + i) << 4));
   }
 }
 
+// Q6_K: ql chunk j byte i = lo4[32j + i] | lo4[32j + 16 + i] << 4; qh chunk j dword m byte b =
+// hi2 of elements 32j + {8m+b, 16+8m+b, 8m+4+b, 16+8m+4+b} at bits 0, 2, 4, 6; scales and d
+// copied (GGUF element e: lo4 from ql[64(e/128) + 32((e%128/32)&1) + e%32] >> 4((e%128/32)>>1),
+// hi2 from qh[32(e/128) + e%32] >> 2(e%128/32)).
 __global__ void k_repack_q6(const uint8_t *src, uint8_t *dst, uint64_t nb) {
-  Q6Planes p = q6_planes(nb);
-  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nb * 210; i += (uint64_t)gridDim.x * blockDim.x) {
-    uint64_t blk = i / 210; uint32_t o = i % 210; uint8_t v = src[i];
-    if (o < 128) dst[p.ql + blk * 128 + o] = v;
-    else if (o < 192) dst[p.qh + blk * 64 + (o - 128)] = v;
-    else if (o < 208) dst[p.sc + blk * 16 + (o - 192)] = v;
-    else dst[p.d + blk * 2 + (o - 208)] = v;
+  const Q6Planes p = q6_planes(nb);
+  for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
+    const uint8_t *b = src + blk * 210;
+    auto lo4 = [&](uint32_t e) -> uint32_t {
+      const uint32_t h = e / 128, t = (e % 128) / 32, l = e % 32;
+      return (b[64 * h + 32 * (t & 1) + l] >> (4 * (t >> 1))) & 15u;
+    };
+    auto hi2 = [&](uint32_t e) -> uint32_t {
+      const uint32_t h = e / 128, t = (e % 128) / 32, l = e % 32;
+      return (b[128 + 32 * h + l] >> (2 * t)) & 3u;
+    };
+    for (uint32_t j = 0; j < 8; j++) {
+      for (uint32_t i = 0; i < 16; i++) dst[p.ql + blk * 128 + 16 * j + i] = (uint8_t)(lo4(32 * j + i) | (lo4(32 * j + 16 + i) << 4));
+      for (uint32_t m = 0; m < 2; m++)
+        for (uint32_t bb = 0; bb < 4; bb++) {
+          const uint32_t e = 32 * j + 8 * m + bb;
+          dst[p.qh + blk * 64 + 8 * j + 4 * m + bb] =
+              (uint8_t)(hi2(e) | (hi2(e + 16) << 2) | (hi2(e + 4) << 4) | (hi2(e + 20) << 6));
+        }
+    }
+    for (int o = 0; o < 16; o++) dst[p.sc + blk * 16 + o] = b[192 + o];
+    dst[p.d + blk * 2] = b[208];
+    dst[p.d + blk * 2 + 1] = b[209];
   }
 }
 __global__ void k_repack_q8(const uint8_t *src, uint8_t *dst, uint64_t nb) {
@@ -123,6 +146,7 @@ __global__ void k_repack_q8(const uint8_t *src, uint8_t *dst, uint64_t nb) {
 hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint64_t blocks) {
   if (!blocks) return hipSuccess;
   uint64_t bytes = blocks * block_bytes(type), grid = (bytes + 255) / 256; if (grid > 65535 * 8) grid = 65535 * 8;
+  if (type != Q8_0) { grid = (blocks + 255) / 256; if (grid > 65535 * 8) grid = 65535 * 8; }
   if (type == Q4_K) hipLaunchKernelGGL(k_repack_q4, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, blocks);
   else if (type == Q6_K) hipLaunchKernelGGL(k_repack_q6, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, blocks);
   else if (type == Q8_0) hipLaunchKernelGGL(k_repack_q8, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, blocks);

@@ -22,6 +22,10 @@ struct wgd_buffer {
   // Weight matrices uploaded with wgd_upload_weights remember their type, shape and layout.
   int layout = LAYOUT_GGUF, type = -1;
   uint32_t cols = 0, rows = 0;
+  // Quantized activations written by wgd_quantize: length and the pending RMSNorm.
+  uint32_t qx_cols = 0;
+  bool qx_normed = false;
+  float qx_eps = 0.f;
 };
 
 static thread_local std::string g_error;
@@ -273,9 +277,9 @@ int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
     int rc = grow(&ctx->mv_qx, &ctx->mv_qx_bytes, qx_bytes(cols), "matvec activation");
     if (rc) return rc;
     QXOut q = qx_view(ctx->mv_qx, cols);
-    rc = ctx_check(ctx, quantize(ctx->stream, (const float *)x->ptr + (uint64_t)input_offset * cols, cols, nullptr, 0.f, q), "matmul");
+    rc = ctx_check(ctx, quantize(ctx->stream, (const float *)x->ptr + (uint64_t)input_offset * cols, cols, nullptr, q), "matmul");
     if (rc) return rc;
-    return ctx_check(ctx, mv(ctx->stream, m, nullptr, qx_const(q), (float *)y->ptr, row_base, MV_STORE), "matmul");
+    return ctx_check(ctx, mv(ctx->stream, m, nullptr, qx_const(q, cols, false, 0.f), (float *)y->ptr + row_base, MV_STORE), "matmul");
   }
   return ctx_check(ctx, matmul(ctx->stream, m, (const float *)x->ptr, (float *)y->ptr, stride, row_base, input_offset, batch), "matmul");
 }
@@ -285,12 +289,17 @@ uint64_t wgd_quantized_bytes(uint32_t cols) { return qx_bytes(cols); }
 int wgd_quantize(wgd_context *ctx, const wgd_buffer *x, uint32_t cols, const wgd_buffer *norm_weight, float epsilon,
                  wgd_buffer *qx) {
   NEED_CTX(ctx); NEED_BUF(ctx, x, "quantize"); NEED_BUF(ctx, qx, "quantize");
-  if (!cols || (cols + 255) / 256 > QX_MAX_TILES) return fail(ctx, WGD_E_INVALID, "quantize: %u columns", cols);
+  if (!cols) return fail(ctx, WGD_E_INVALID, "quantize: 0 columns");
   NEED_FIT(ctx, x, (uint64_t)cols * 4, "quantize input");
   NEED_FIT(ctx, qx, qx_bytes(cols), "quantized activation");
   if (norm_weight) { NEED_BUF(ctx, norm_weight, "quantize"); NEED_FIT(ctx, norm_weight, (uint64_t)cols * 4, "norm weight"); }
-  return ctx_check(ctx, quantize(ctx->stream, (const float *)x->ptr, cols, norm_weight ? (const float *)norm_weight->ptr : nullptr,
-                                 epsilon, qx_view(qx->ptr, cols)), "quantize");
+  int rc = ctx_check(ctx, quantize(ctx->stream, (const float *)x->ptr, cols, norm_weight ? (const float *)norm_weight->ptr : nullptr,
+                                    qx_view(qx->ptr, cols)), "quantize");
+  if (rc) return rc;
+  qx->qx_cols = cols;
+  qx->qx_normed = norm_weight != nullptr;
+  qx->qx_eps = epsilon;
+  return WGD_OK;
 }
 
 int wgd_matvec(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *qx, wgd_buffer *y, uint32_t cols,
@@ -305,7 +314,9 @@ int wgd_matvec(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
   if (w->layout != LAYOUT_GGUF && (w->type != type || w->cols != cols || w->rows != rows))
     return fail(ctx, WGD_E_INVALID, "matvec: weights %s were uploaded as type %d, %ux%u", w->label.c_str(), w->type, w->cols, w->rows);
   if (!mv_supported(m)) return fail(ctx, WGD_E_INVALID, "matvec: type %d in this layout has no quantized matvec (upload with wgd_upload_weights)", type);
-  return ctx_check(ctx, mv(ctx->stream, m, nullptr, qx_const(qx_view(qx->ptr, cols)), (float *)y->ptr, row_base, MV_STORE), "matvec");
+  if (qx->qx_cols != cols) return fail(ctx, WGD_E_INVALID, "matvec: %s holds no quantized row of %u columns (wgd_quantize first)", qx->label.c_str(), cols);
+  const QXView xv = qx_const(qx_view(qx->ptr, cols), cols, qx->qx_normed, qx->qx_eps);
+  return ctx_check(ctx, mv(ctx->stream, m, nullptr, xv, (float *)y->ptr + row_base, MV_STORE), "matvec");
 }
 
 int wgd_dequant(wgd_context *ctx, int32_t type, const wgd_buffer *w, wgd_buffer *out, uint64_t count) {
