@@ -1,0 +1,35 @@
+// attention.h — the decode-step attention of one token (attention.hip).
+#pragma once
+#include "internal.h"
+#include "matvec.h"
+
+namespace wgd {
+
+// One generated token at the device-resident position *pos: per-head Q/K RMSNorm and RoPE of
+// the new q and k (rope mode as wgd::rope: 0 Q/K norm + half-split, 1 half-split, 2 adjacent
+// pairs), the K/V append to ring slot pos % capacity, and attention of every query head over
+// keys [pos + 1 - min(pos + 1, window), pos + 1) (attentionShader, shaders.ts:88-122).
+// The output is written as f32 y[heads * hd] and, when qx.d0 is set, quantized for the O
+// projection.
+struct DecodeAttnArgs {
+  const float *q, *k, *v;        // projections of the token, before RoPE: [heads][hd], [kvh][hd]
+  float *kc, *vc;                // ring [capacity][kvh][hd]
+  const float *q_norm, *k_norm;  // mode 0 weights
+  float *partial;                // decode_attention_scratch_floats()
+  float *y;
+  QXOut qx;
+  const int32_t *pos;
+  const float2 *rope_table;      // (cos, sin) per position and rotation pair, or null
+  uint32_t rope_positions;       // positions the table covers
+  uint32_t heads, kv_heads, hd, rot, capacity, window;
+  float scale, theta, rope_scale, eps;
+  int mode;
+};
+bool decode_attention_supported(uint32_t heads, uint32_t kv_heads, uint32_t hd);
+uint64_t decode_attention_scratch_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t capacity);
+hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &a);
+// tab[p * (rot/2) + i] = (cos, sin) of p * scale * theta^(-2i/rot), the angle formed in f64
+// as in wgd::rope, for p < positions.
+hipError_t rope_table(hipStream_t s, float2 *tab, uint32_t positions, uint32_t rot, float theta, float scale);
+
+}  // namespace wgd

@@ -13,6 +13,7 @@
 // second kernel merges the splits. Tile size T keeps T*hd = 4096 floats per operand.
 #include "internal.h"
 #include "decode.h"
+#include "attention.h"
 
 namespace wgd {
 
@@ -224,6 +225,314 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
     WGD_HIP(hipGetLastError());
   }
   return hipSuccess;
+}
+
+// ------------------------------------------------------------------ decode step
+//
+// One token: a workgroup per (kv head, chunk of 32 * NB keys), four wavefronts of KPB-key
+// batches. The prologue normalises and rotates the group's query heads and the new key
+// (angles in f64 as in k_rope) into LDS; the workgroup whose chunk holds the current
+// position writes the new key and value into the ring (the slot of the position,
+// pos % capacity: the ring keeps at least the window, so no other chunk of this launch
+// reads it) and uses the fresh values for that key. Lanes span the head dimension (EL
+// floats each): a key row is one coalesced load, each score a DPP wave sum broadcast as a
+// scalar, and the online softmax state (m, l) is uniform per wavefront. The four
+// wavefronts merge through LDS and the workgroup leaves (max, sum, unnormalised output)
+// per query head; k_attn_comb merges the chunks.
+constexpr uint32_t AD_KPB = 8;   // keys per wavefront batch
+constexpr uint32_t AD_WAVES = 4;
+
+struct AttnDecK {
+  const float *q, *k, *v; float *kc, *vc; const float *qn, *kn; float *part;
+  const int32_t *pos;
+  const float2 *tab; uint32_t tab_pos;
+  uint32_t heads, kvh, rot, cap, window, group, chunk, nsplit;
+  float scale, theta, rscale, eps; int mode;
+};
+
+template <int EL, int G>
+__global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
+  constexpr uint32_t HD = 64 * EL;
+  __shared__ float vec[(G + 1) * HD];        // query heads, then the new key
+  __shared__ float csn[HD];                   // cos / sin per rotation pair
+  __shared__ float wm[AD_WAVES][G], wl[AD_WAVES][G];
+  __shared__ float wo[AD_WAVES][G][HD];
+  const uint32_t lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t kv = blockIdx.x, z = blockIdx.y, g = a.group;
+  const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane(*a.pos);
+  const uint32_t end = pos + 1, win = end < a.window ? end : a.window, begin = end - win;
+  const uint32_t lo = begin + z * a.chunk;
+  if (lo >= end) return;
+  const uint32_t hi = lo + a.chunk < end ? lo + a.chunk : end;
+  const uint32_t nb = a.chunk / (AD_WAVES * AD_KPB);
+  const uint64_t rowf = (uint64_t)a.kvh * HD;  // floats per ring slot
+  // ---- key batch loads (rows past the chunk re-read its first key; they are masked)
+  float kr[AD_KPB][EL], vr[AD_KPB][EL];
+  auto load_batch = [&](uint32_t b) {
+#pragma unroll
+    for (uint32_t k = 0; k < AD_KPB; k++) {
+      uint32_t t = lo + (b * AD_WAVES + w) * AD_KPB + k;
+      if (t >= hi) t = lo;
+      const uint64_t base = (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD + lane * EL;
+#pragma unroll
+      for (int e = 0; e < EL; e++) { kr[k][e] = a.kc[base + e]; vr[k][e] = a.vc[base + e]; }
+    }
+  };
+  load_batch(0);
+  // ---- prologue: Q/K norm and RoPE of the group's query heads and the new key
+  const uint32_t half = a.rot / 2;
+  for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
+    if (a.tab && pos < a.tab_pos) {
+      const float2 cs = a.tab[(uint64_t)pos * half + i];
+      csn[2 * i] = cs.x;
+      csn[2 * i + 1] = cs.y;
+    } else {
+      const double angle = (double)pos * (double)a.rscale * pow((double)a.theta, -(double)(2 * i) / (double)a.rot);
+      double sd, cd;
+      sincos(angle, &sd, &cd);
+      csn[2 * i] = (float)cd;
+      csn[2 * i + 1] = (float)sd;
+    }
+  }
+  for (uint32_t it = w; it <= g; it += AD_WAVES) {
+    const bool isk = it == g;
+    const float *src = isk ? a.k + (uint64_t)kv * HD : a.q + ((uint64_t)kv * g + it) * HD;
+    float x[EL];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EL; e++) { x[e] = src[lane * EL + e]; ss += x[e] * x[e]; }
+    if (a.mode == 0) {
+      const float inv = 1.f / sqrtf(wave_total(ss) / (float)HD + a.eps);
+      const float *wn = isk ? a.kn : a.qn;
+#pragma unroll
+      for (int e = 0; e < EL; e++) x[e] = x[e] * wn[lane * EL + e] * inv;
+    }
+#pragma unroll
+    for (int e = 0; e < EL; e++) vec[it * HD + lane * EL + e] = x[e];
+  }
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < (g + 1) * half; j += blockDim.x) {
+    const uint32_t it = j / half, i = j % half;
+    const uint32_t ia = a.mode == 2 ? 2 * i : i, ib = a.mode == 2 ? 2 * i + 1 : i + half;
+    float *v = vec + it * HD;
+    const float c = csn[2 * i], sn = csn[2 * i + 1], xa = v[ia], xb = v[ib];
+    v[ia] = xa * c - xb * sn;
+    v[ib] = xa * sn + xb * c;
+  }
+  __syncthreads();
+  const bool mine = pos >= lo && pos < hi;
+  if (mine) {
+    const uint64_t slot = (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
+    for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x) {
+      a.kc[slot + d] = vec[g * HD + d];
+      a.vc[slot + d] = a.v[(uint64_t)kv * HD + d];
+    }
+  }
+  float qr[G][EL], kf[EL], vf[EL];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int e = 0; e < EL; e++) qr[i][e] = (uint32_t)i < g ? vec[i * HD + lane * EL + e] : 0.f;
+#pragma unroll
+  for (int e = 0; e < EL; e++) { kf[e] = vec[g * HD + lane * EL + e]; vf[e] = a.v[(uint64_t)kv * HD + lane * EL + e]; }
+  // ---- keys
+  float m[G], l[G], o[G][EL];
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    m[i] = -INFINITY; l[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EL; e++) o[i][e] = 0.f;
+  }
+  for (uint32_t b = 0; b < nb; b++) {
+    if (b > 0) load_batch(b);
+    const uint32_t t0 = lo + (b * AD_WAVES + w) * AD_KPB;
+    if (t0 >= hi) break;  // uniform: later batches of this wavefront are past the chunk too
+    float sc[AD_KPB][G];
+#pragma unroll
+    for (uint32_t k = 0; k < AD_KPB; k++) {
+      const bool fresh = t0 + k == pos;
+#pragma unroll
+      for (int e = 0; e < EL; e++) {
+        if (fresh) { kr[k][e] = kf[e]; vr[k][e] = vf[e]; }
+      }
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < EL; e++) d += qr[i][e] * kr[k][e];
+        sc[k][i] = t0 + k < hi ? wave_total(d) * a.scale : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      float bm = sc[0][i];
+#pragma unroll
+      for (uint32_t k = 1; k < AD_KPB; k++) bm = fmaxf(bm, sc[k][i]);
+      const float mn = fmaxf(m[i], bm);  // finite: key t0 is inside the chunk
+      const float corr = m[i] == -INFINITY ? 0.f : expf(m[i] - mn);
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < EL; e++) o[i][e] *= corr;
+#pragma unroll
+      for (uint32_t k = 0; k < AD_KPB; k++) {
+        const float p = sc[k][i] == -INFINITY ? 0.f : expf(sc[k][i] - mn);
+        ps += p;
+#pragma unroll
+        for (int e = 0; e < EL; e++) o[i][e] += p * vr[k][e];
+      }
+      l[i] = l[i] * corr + ps;
+      m[i] = mn;
+    }
+  }
+  // ---- merge the wavefronts
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    if (lane == 0) { wm[w][i] = m[i]; wl[w][i] = l[i]; }
+#pragma unroll
+    for (int e = 0; e < EL; e++) wo[w][i][lane * EL + e] = o[i][e];
+  }
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < g * HD; j += blockDim.x) {
+    const uint32_t i = j / HD, d = j % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) M = fmaxf(M, wm[u][i]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) {
+      if (wm[u][i] == -INFINITY) continue;
+      const float f = expf(wm[u][i] - M);
+      L += wl[u][i] * f;
+      O += wo[u][i][d] * f;
+    }
+    float *pp = a.part + (((uint64_t)kv * g + i) * a.nsplit + z) * (HD + 2);
+    if (d == 0) { pp[0] = M; pp[1] = L; }
+    pp[2 + d] = O;
+  }
+}
+
+// Merge of the chunks of one query head: thread d owns output element d. The partials were
+// written by the previous launch (other XCDs' L2), so every load is issued before any is
+// used: one round trip for the (max, sum) pairs, one per 16 chunks for the outputs.
+constexpr uint32_t AD_MAX_SPLITS = 1024;
+__global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, QXOut qx, const int32_t *pos_dev,
+                                                   uint32_t window, uint32_t chunk, uint32_t nsplit, uint32_t hd) {
+  __shared__ float wz[AD_MAX_SPLITS];
+  __shared__ float red[8];
+  const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wv = d >> 6, nw = (blockDim.x + 63) >> 6;
+  const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane(*pos_dev);
+  const uint32_t end = pos + 1, win = end < window ? end : window;
+  const uint32_t nact = (win + chunk - 1) / chunk;
+  const float *pp = part + (uint64_t)h * nsplit * (hd + 2);
+  // (max, sum) of chunk z in thread z
+  float mz = -INFINITY, lz = 0.f;
+  for (uint32_t z = d; z < nact; z += blockDim.x) {
+    mz = fmaxf(mz, pp[(uint64_t)z * (hd + 2)]);
+  }
+  float M = mz;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  if (lane == 0) red[wv] = M;
+  __syncthreads();
+  M = red[0];
+  for (uint32_t u = 1; u < nw; u++) M = fmaxf(M, red[u]);
+  float L = 0.f;
+  for (uint32_t z = d; z < nact; z += blockDim.x) {
+    const float f = expf(pp[(uint64_t)z * (hd + 2)] - M);
+    wz[z] = f;
+    lz += pp[(uint64_t)z * (hd + 2) + 1] * f;
+  }
+  L = wave_sum(lz);
+  __syncthreads();
+  if (lane == 0) red[wv] = L;
+  __syncthreads();
+  L = 0.f;
+  for (uint32_t u = 0; u < nw; u++) L += red[u];
+  float O = 0.f;
+  if (d < hd) {
+    uint32_t z = 0;
+    for (; z + 16 <= nact; z += 16) {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; k++) v[k] = pp[(uint64_t)(z + k) * (hd + 2) + 2 + d];
+#pragma unroll
+      for (int k = 0; k < 16; k++) O += v[k] * wz[z + k];
+    }
+    for (; z < nact; z++) O += pp[(uint64_t)z * (hd + 2) + 2 + d] * wz[z];
+  }
+  const float out = O / L;
+  if (d < hd) y[(uint64_t)h * hd + d] = out;
+  if (qx.d0) qx_store(qx, h * hd + d, out, out, d < hd);
+}
+
+__global__ void k_rope_table(float2 *tab, uint32_t positions, uint32_t half, uint32_t rot, float theta, float scale) {
+  const uint64_t n = (uint64_t)positions * half;
+  for (uint64_t j = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; j < n; j += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t p = (uint32_t)(j / half), i = (uint32_t)(j % half);
+    const double angle = (double)p * (double)scale * pow((double)theta, -(double)(2 * i) / (double)rot);
+    double sd, cd;
+    sincos(angle, &sd, &cd);
+    tab[j] = make_float2((float)cd, (float)sd);
+  }
+}
+
+hipError_t rope_table(hipStream_t s, float2 *tab, uint32_t positions, uint32_t rot, float theta, float scale) {
+  if (!positions || rot < 2 || rot % 2) return hipErrorInvalidValue;
+  const uint64_t n = (uint64_t)positions * (rot / 2);
+  uint64_t grid = (n + 255) / 256;
+  if (grid > 65535) grid = 65535;
+  hipLaunchKernelGGL(k_rope_table, dim3((uint32_t)grid), dim3(256), 0, s, tab, positions, rot / 2, rot, theta, scale);
+  return hipGetLastError();
+}
+
+static uint32_t dec_chunk(uint32_t capacity, uint32_t kvh) {
+  // enough workgroups to cover the chip twice at full context, at most 512 keys each
+  uint32_t nb = capacity * kvh / (AD_WAVES * AD_KPB * 2 * (uint32_t)device_cu_count());
+  if (nb < 1) nb = 1;
+  if (nb > 16) nb = 16;
+  return nb * AD_WAVES * AD_KPB;
+}
+
+bool decode_attention_supported(uint32_t heads, uint32_t kv_heads, uint32_t hd) {
+  return (hd == 64 || hd == 128 || hd == 256) && kv_heads && heads % kv_heads == 0 && heads / kv_heads <= 8;
+}
+
+uint64_t decode_attention_scratch_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t capacity) {
+  const uint32_t chunk = dec_chunk(capacity, kv_heads);
+  return (uint64_t)heads * ((capacity + chunk - 1) / chunk) * (hd + 2);
+}
+
+template <int EL>
+static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
+  if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec<EL, 1>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec<EL, 2>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec<EL, 4>), grid, dim3(256), 0, s, k);
+  else hipLaunchKernelGGL((k_attn_dec<EL, 8>), grid, dim3(256), 0, s, k);
+}
+
+hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
+  if (!decode_attention_supported(in.heads, in.kv_heads, in.hd) || !in.capacity || !in.window || !in.pos ||
+      !in.partial || (in.mode == 0 && (!in.q_norm || !in.k_norm)) || in.rot > in.hd || in.rot % 2)
+    return hipErrorInvalidValue;
+  AttnDecK k;
+  k.q = in.q; k.k = in.k; k.v = in.v; k.kc = in.kc; k.vc = in.vc; k.qn = in.q_norm; k.kn = in.k_norm;
+  k.part = in.partial; k.pos = in.pos; k.tab = in.rope_table; k.tab_pos = in.rope_table ? in.rope_positions : 0;
+  k.heads = in.heads; k.kvh = in.kv_heads; k.rot = in.rot ? in.rot : in.hd; k.cap = in.capacity;
+  k.window = in.window; k.group = in.heads / in.kv_heads;
+  k.chunk = dec_chunk(in.capacity, in.kv_heads);
+  const uint32_t keys = in.window < in.capacity ? in.window : in.capacity;
+  k.nsplit = (keys + k.chunk - 1) / k.chunk;
+  if (k.nsplit > AD_MAX_SPLITS) return hipErrorInvalidValue;
+  k.scale = in.scale; k.theta = in.theta; k.rscale = in.rope_scale; k.eps = in.eps; k.mode = in.mode;
+  const dim3 grid(in.kv_heads, k.nsplit);
+  if (in.hd == 64) launch_dec<1>(s, k, grid);
+  else if (in.hd == 128) launch_dec<2>(s, k, grid);
+  else launch_dec<4>(s, k, grid);
+  WGD_HIP(hipGetLastError());
+  const uint32_t threads = (in.hd + 63) / 64 * 64;
+  hipLaunchKernelGGL(k_attn_comb, dim3(in.heads), dim3(threads), 0, s, (const float *)in.partial, in.y, in.qx,
+                     in.pos, in.window, k.chunk, k.nsplit, in.hd);
+  return hipGetLastError();
 }
 
 }  // namespace wgd

@@ -58,16 +58,19 @@ __device__ __forceinline__ float deq_elem(int type, const uint8_t *b, uint64_t i
 }
 
 // ------------------------------------------------------------------ planar chunk layouts
-// (written by repack_planar, quant.hip). Chunk ci = block * 8 + sub-block holds 32 elements.
+// (written by repack_planar, quant.hip): chunk (row, c) of 32 elements in a tiled plane.
 
-// Q4_K quant of element e (0..31) of chunk ci: byte e % 16, nibble e / 16.
-__device__ __forceinline__ uint32_t q4_quant(const uint8_t *w, uint64_t ci, uint32_t e) {
-  return (w[ci * 16 + (e & 15)] >> (4 * (e >> 4))) & 15u;
+// Q4_K quant of element k of `row` (C chunks per row): chunk k / 32, byte k % 16, nibble (k % 32) / 16.
+__device__ __forceinline__ uint32_t q4_quant(const uint8_t *w, uint32_t row, uint32_t C, uint32_t k) {
+  const uint32_t e = k % 32;
+  return (w[tiled(row, k / 32, C) * 16 + (e & 15)] >> (4 * (e >> 4))) & 15u;
 }
-// Q6_K 6-bit quant of element e (0..31) of chunk ci: low nibble as Q4_K in the ql plane; the
-// high 2 bits in qh byte 4 * ((e % 16) / 8) + e % 4 at bit 4 * ((e % 8) / 4) + 2 * (e / 16).
-__device__ __forceinline__ uint32_t q6_quant(const uint8_t *w, uint64_t nbt, uint64_t ci, uint32_t e) {
-  const Q6Planes p = q6_planes(nbt);
+// Q6_K 6-bit quant of element k: low nibble as Q4_K in the ql plane; the high 2 bits of chunk
+// element e in qh byte 4 * ((e % 16) / 8) + e % 4 at bit 4 * ((e % 8) / 4) + 2 * (e / 16).
+__device__ __forceinline__ uint32_t q6_quant(const uint8_t *w, uint64_t nbp, uint32_t row, uint32_t C, uint32_t k) {
+  const Q6Planes p = q6_planes(nbp);
+  const uint32_t e = k % 32;
+  const uint64_t ci = tiled(row, k / 32, C);
   const uint32_t lo = (w[p.ql + ci * 16 + (e & 15)] >> (4 * (e >> 4))) & 15u;
   const uint32_t r = e & 15;
   const uint32_t hi = (w[p.qh + ci * 8 + 4 * (r >> 3) + (r & 3)] >> (4 * ((r & 7) >> 2) + 2 * (e >> 4))) & 3u;
@@ -81,6 +84,31 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+
+// Sum over aligned segments of `width` lanes (16, 32 or 64) with DPP moves, which stay in
+// the VALU (no LDS crossbar round trip per step): quad xor 1, quad xor 2, half-row mirror and
+// row mirror leave each 16-lane row's sum in all of its lanes; row_bcast15 / row_bcast31
+// fold rows into rows 1, 3 and then 3. The segment sum ends in its last lane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float seg_sum(float v, uint32_t width) {
+  v = dpp_add<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xf>(v);  // row_mirror
+  if (width >= 32) v = dpp_add<0x142, 0xa>(v);  // row_bcast15 into rows 1 and 3
+  if (width == 64) v = dpp_add<0x143, 0xc>(v);  // row_bcast31 into rows 2 and 3
+  return v;
+}
+
+// Wave-wide sum, the same value returned in every lane (DPP folds into lane 63, then a
+// scalar read).
+__device__ __forceinline__ float wave_total(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(seg_sum(v, 64)), 63));
+}
+
 // Sum within aligned segments of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float segment_sum(float v, int width) {
   for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -63,12 +63,11 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
     return;
   }
   if (a.type == Q4_K && a.layout == LAYOUT_PLANAR) {
-    Q4Planes p = q4_planes(a.nbt);
-    const uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
-    const uint32_t j = k & 255, s = j >> 5, e0 = j & 31;
-    uint4 h = *(const uint4 *)(a.w + p.hdr + bi * 16);
-    // chunk s, bytes e0 % 16 .. +8, nibble e0 / 16
-    uint2 qv = *(const uint2 *)(a.w + p.qs + (bi * 8 + s) * 16 + (e0 & 15));
+    const Q4Planes p = q4_planes(a.nbt);
+    const uint32_t j = k & 255, s = j >> 5, e0 = k & 31;
+    uint4 h = *(const uint4 *)(a.w + p.hdr + tiled(row, k >> 8, a.bpr) * 16);
+    // chunk k / 32, bytes e0 % 16 .. +8, nibble e0 / 16
+    uint2 qv = *(const uint2 *)(a.w + p.qs + tiled(row, k >> 5, a.bpr * 8) * 16 + (e0 & 15));
     uint32_t A = h.y, B = h.z, C = h.w, sh = 8 * (s & 3), sc, m;
     if (s < 4) { sc = (A >> sh) & 63u; m = (B >> sh) & 63u; }
     else { sc = ((C >> sh) & 15u) | (((A >> sh) >> 6 & 3u) << 4); m = ((C >> sh) >> 4 & 15u) | (((B >> sh) >> 6 & 3u) << 4); }
@@ -82,15 +81,14 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
     return;
   }
   if (a.type == Q6_K && a.layout == LAYOUT_PLANAR) {
-    Q6Planes p = q6_planes(a.nbt);
-    const uint64_t bi = (uint64_t)row * a.bpr + (k >> 8);
-    const uint32_t j = k & 255, s = j >> 5, e0 = j & 31, h = e0 >> 4;
-    const uint64_t ci = bi * 8 + s;
+    const Q6Planes p = q6_planes(a.nbt);
+    const uint32_t e0 = k & 31, h = e0 >> 4;
+    const uint64_t ci = tiled(row, k >> 5, a.bpr * 8);
     uint2 lo = *(const uint2 *)(a.w + p.ql + ci * 16 + (e0 & 15));
     // high bits of elements e0 .. e0+7: qh dword (e0 % 16) / 8, byte i % 4, bit 4 * (i / 4) + 2h
     uint32_t hq = *(const uint32_t *)(a.w + p.qh + ci * 8 + 4 * ((e0 & 15) >> 3));
     float sc = (float)(int8_t)a.w[p.sc + ci * 2 + h];
-    float d = half_bits(*(const uint16_t *)(a.w + p.d + bi * 2)) * sc;
+    float d = half_bits(*(const uint16_t *)(a.w + p.d + tiled(row, k >> 8, a.bpr) * 2)) * sc;
     uint32_t ls = 4 * h;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -101,10 +99,9 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
     return;
   }
   if (a.type == Q8_0 && a.layout == LAYOUT_PLANAR) {
-    Q8Planes p = q8_planes(a.nbt);
-    uint64_t bi = (uint64_t)row * a.bpr + (k >> 5);
-    uint2 q = *(const uint2 *)(a.w + p.qs + bi * 32 + (k & 31));
-    float d = half_bits(*(const uint16_t *)(a.w + p.d + bi * 2));
+    const Q8Planes p = q8_planes(a.nbt);
+    uint2 q = *(const uint2 *)(a.w + p.qs + tiled(row, k >> 4, a.bpr * 2) * 16 + (k & 15));
+    float d = half_bits(*(const uint16_t *)(a.w + p.d + tiled(row, k >> 5, a.bpr) * 2));
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = d * (float)(int8_t)(((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xFFu);
     return;
@@ -190,7 +187,7 @@ hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32
   GemmArgs a;
   a.w = w.data; a.type = w.type; a.layout = w.layout;
   a.rb = row_bytes(w.type, w.cols); a.bpr = w.cols / block_size(w.type);
-  a.nbt = (uint64_t)a.bpr * w.rows;
+  a.nbt = (uint64_t)a.bpr * (w.layout == LAYOUT_PLANAR ? tile_rows(w.rows) : w.rows);
   a.x = x; a.y = y; a.cols = w.cols; a.rows = w.rows; a.stride = stride; a.row_base = row_base;
   a.input_offset = input_offset; a.batch = batch;
   dim3 grid((w.rows + 63) / 64, (batch + NT - 1) / NT);

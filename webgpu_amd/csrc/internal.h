@@ -27,9 +27,12 @@ inline int block_bytes(int t) {
 inline uint64_t row_bytes(int t, uint64_t cols) { return cols / block_size(t) * block_bytes(t); }
 
 // Device layouts of a weight matrix. GGUF keeps the file's block bytes. The planar
-// layouts split each block's fields into 16-byte-aligned planes (same bytes, same
-// decoded values) so 210-byte Q6_K and 34-byte Q8_0 blocks can be read with aligned
-// vector loads; the planes are laid out one after another in one allocation.
+// layouts (Q4_K, Q6_K, Q8_0) hold the same bits rearranged for the decode matvec: the
+// quants of each 32 consecutive elements of a row (16 for Q8_0) form a 16-byte "chunk"
+// (C chunks per row), the per-block fields (Q4_K header, Q6_K high bits / scales / d,
+// Q8_0 d) live in separate planes, and rows are grouped in tiles of 16: within a tile,
+// the 16 rows' entries of one column are consecutive, so 16 rows x 4 columns of chunks
+// are 1 KB of contiguous bytes. Rows are padded to a multiple of 16 (zero bytes).
 enum Layout : int { LAYOUT_GGUF = 0, LAYOUT_PLANAR = 1 };
 
 struct Matrix {
@@ -39,17 +42,26 @@ struct Matrix {
   uint32_t cols = 0, rows = 0;
 };
 
-// Planar plane offsets for a matrix of nb blocks.
+// Entry (row, col) of a tiled plane with ncols columns.
+__host__ __device__ inline uint64_t tiled(uint64_t row, uint64_t col, uint64_t ncols) {
+  return ((row >> 4) * ncols + col) * 16 + (row & 15);
+}
+__host__ __device__ inline uint64_t tile_rows(uint64_t rows) { return (rows + 15) / 16 * 16; }
+// Plane offsets for nbp blocks (padded rows x blocks per row).
 struct Q4Planes { uint64_t qs, hdr; };
-__host__ __device__ inline Q4Planes q4_planes(uint64_t nb) { return {0, nb * 128}; }
+__host__ __device__ inline Q4Planes q4_planes(uint64_t nbp) { return {0, nbp * 128}; }
 struct Q6Planes { uint64_t ql, qh, sc, d; };
-__host__ __device__ inline Q6Planes q6_planes(uint64_t nb) { return {0, nb * 128, nb * 192, nb * 208}; }
+__host__ __device__ inline Q6Planes q6_planes(uint64_t nbp) { return {0, nbp * 128, nbp * 192, nbp * 208}; }
 struct Q8Planes { uint64_t qs, d; };
-__host__ __device__ inline Q8Planes q8_planes(uint64_t nb) { return {0, nb * 32}; }
+__host__ __device__ inline Q8Planes q8_planes(uint64_t nbp) { return {0, nbp * 32}; }
+__host__ __device__ inline uint32_t chunk_elems(int type) { return type == Q8_0 ? 16u : 32u; }
 
-// Rewrites GGUF blocks into the planar layout (device to device).
-hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint64_t blocks);
 bool has_planar(int type);
+// Bytes of a planar matrix (rows padded to 16).
+uint64_t planar_bytes(int type, uint32_t cols, uint32_t rows);
+// Rewrites a GGUF matrix (rows x cols) into the planar layout (device to device); dst must
+// hold planar_bytes and be zero-filled (padding rows).
+hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint32_t cols, uint32_t rows);
 
 // ---------------------------------------------------------------- launchers
 

@@ -28,6 +28,37 @@ uint64_t qx_bytes(uint32_t K);
 QXOut qx_view(void *base, uint32_t K);
 QXView qx_const(const QXOut &q, uint32_t K, bool normed, float eps);
 
+#ifdef __HIPCC__
+// Quantizes one value per lane in aligned 16-lane groups; the block scale is max|v| / 127.
+__device__ __forceinline__ void quant_lane16(float v, float &scale, int &d0, int &d1, int &d2) {
+  float a = fabsf(v);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  scale = a * (1.f / 127.f);
+  const float u = a > 0.f ? v * (127.f / a) : 0.f;
+  const float r0 = fminf(fmaxf(rintf(u), -127.f), 127.f);
+  const float t = (u - r0) * 254.f;
+  const float r1 = fminf(fmaxf(rintf(t), -127.f), 127.f);
+  const float t2 = (t - r1) * 254.f;
+  const float r2 = fminf(fmaxf(rintf(t2), -127.f), 127.f);
+  d0 = (int)r0; d1 = (int)r1; d2 = (int)r2;
+}
+
+// Writes element `i` of a QX vector: v is the stored value (already times any norm
+// weight), raw the value whose square is summed. Lanes hold 16 consecutive aligned elements.
+__device__ __forceinline__ void qx_store(const QXOut &q, uint32_t i, float v, float raw, bool live) {
+  float sc; int d0, d1, d2;
+  quant_lane16(live ? v : 0.f, sc, d0, d1, d2);
+  float s16 = live ? v : 0.f, q16 = live ? raw * raw : 0.f;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) { s16 += __shfl_xor(s16, o, 64); q16 += __shfl_xor(q16, o, 64); }
+  if (live) {
+    q.d0[i] = (int8_t)d0; q.d1[i] = (int8_t)d1; q.d2[i] = (int8_t)d2;
+    if ((i & 15) == 0) { q.scale[i >> 4] = sc; q.sum[i >> 4] = s16; q.sq[i >> 4] = q16; }
+  }
+}
+#endif
+
 // x (length K, K % 16 == 0) -> QX; with norm_w the stored values are x * norm_w.
 hipError_t quantize(hipStream_t s, const float *x, uint32_t K, const float *norm_w, const QXOut &q);
 
@@ -49,28 +80,30 @@ struct MVTarget {
   const float *bias = nullptr;
 };
 
-// Launch shape: a workgroup owns RT rows; its NS x NR wavefronts split K into NS slices and
-// the rows into NR groups. Wc lanes share a row (P = 64 / Wc rows per load instruction);
-// each lane owns NSB chunk columns of its slice and walks ITER row steps of its group, D
-// row steps in flight.
-struct MVPlan { uint32_t C, Wc, P, NS, NSB, NR, ITER, D, RT, tiles, threads; };
+// Launch shape. A wavefront computes 16 rows x 4 chunk columns per MFMA "unit" (lane = row
+// r % 16, column group g); a workgroup owns RT = 16 * NR * ITER rows, its NS x NR wavefronts
+// split K into NS slices of NSB units (4 * NSB chunk columns) and the row tiles into NR
+// groups of ITER steps; each wavefront runs its U = ITER * NSB units with DU in flight.
+struct MVPlan { uint32_t C, NS, NSB, NR, ITER, DU, RT, tiles, threads, lds; };
 
 constexpr int MV_MAX_SEGS = 3;
 struct MVSeg {
   const uint8_t *w, *w1;
   uint32_t bytes;      // allocation size (buffer range)
-  uint32_t nbt;        // blocks in the matrix (plane offsets)
+  uint32_t nbp;        // blocks of the padded matrix (plane offsets)
+  uint32_t bpr;        // blocks per row
+  uint32_t rows, tiles;
   float *y;
   const float *bias;
-  uint32_t rows, tiles;
 };
 struct MV {
   MVSeg seg[MV_MAX_SEGS];
   uint32_t nseg;
   QXView x;
-  uint32_t C, Wc, wshift, P, NS, NR, ITER, RT;
+  uint32_t C, ke;      // chunk columns; staged activation elements (NS * NSB * 4 chunks)
+  uint32_t NS, NSB, NR, ITER, RT, U;
   int epi;
-  QXOut oq;               // re-quantization of the output (single-matrix launches)
+  QXOut oq;            // re-quantization of the output (single-matrix launches)
   const float *oq_norm;
 };
 

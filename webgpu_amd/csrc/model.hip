@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "internal.h"
+#include "attention.h"
 #include "matvec.h"
 #include "model.h"
 
@@ -67,6 +68,9 @@ struct wgd_model {
   // Quantized-activation decode path (every matrix Q4_K, Q6_K or Q8_0): activation buffers
   // in the QX format.
   bool qpath = false;
+  bool fused_attention = false;  // decode attention in one pass (head dims 64 / 128 / 256)
+  // RoPE (cos, sin) tables of the decode attention: [0] the model's theta, [1] Gemma's local
+  float2 *rope_tab[2] = {nullptr, nullptr};
   void *qx_attn = nullptr, *qx_ffn = nullptr, *qx_o = nullptr, *qx_down = nullptr, *qx_head = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -124,6 +128,31 @@ hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, cons
   a.scale = c.attention_scale; a.window = window_of(m, l); a.capacity = L.cap; a.batch = n;
   a.partial = m->att_part; a.partial_floats = (uint32_t)m->att_part_floats;
   return attention(s, a);
+}
+
+// The decode token's attention in one fused pass (Q/K norm, RoPE, KV append, attention,
+// merge), writing m->att and its quantized form for the O projection.
+hipError_t decode_attention_layer(wgd_model *m, int l, const QXOut &qx) {
+  const wgd_model_config &c = m->c;
+  Layer &L = m->L[l];
+  DecodeAttnArgs a;
+  a.q = m->q; a.k = m->k; a.v = m->v; a.kc = L.kc; a.vc = L.vc;
+  a.q_norm = nullptr; a.k_norm = nullptr;
+  a.partial = m->att_part; a.y = m->att; a.qx = qx; a.pos = &m->state->pos;
+  a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = c.head_dim; a.capacity = L.cap; a.window = window_of(m, l);
+  a.scale = c.attention_scale; a.eps = c.epsilon;
+  a.rope_table = m->rope_tab[0]; a.rope_positions = (uint32_t)c.context;
+  if (is_gemma(m)) {
+    a.mode = 0; a.rot = 0; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
+    a.theta = local_layer(m, l) ? c.local_theta : c.theta;
+    a.rope_scale = local_layer(m, l) ? 1.f : c.rope_scale;
+    if (local_layer(m, l)) a.rope_table = m->rope_tab[1];
+  } else if (c.qk_norm) {
+    a.mode = 0; a.rot = c.rotary_dim; a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.theta = c.theta; a.rope_scale = c.rope_scale;
+  } else {
+    a.mode = c.rope_adjacent ? 2 : 1; a.rot = c.rotary_dim; a.theta = c.theta; a.rope_scale = c.rope_scale;
+  }
+  return decode_attention(m->ctx->stream, a);
 }
 
 // n tokens already gathered into m->hidden (a prompt chunk, or one decode token on the
@@ -219,8 +248,12 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
     qkv[1].w = &L.k; qkv[1].y = m->k; qkv[1].bias = L.bk;
     qkv[2].w = &L.v; qkv[2].y = m->v; qkv[2].bias = L.bv;
     WGD_HIP(mv_group(s, qkv, 3, qv(m->qx_attn, H, true, c.epsilon)));
-    WGD_HIP(attention_block(m, l, 1, 0, pos));
-    WGD_HIP(quantize(s, m->att, qd, nullptr, qx_view(m->qx_o, qd)));
+    if (m->fused_attention) {
+      WGD_HIP(decode_attention_layer(m, l, qx_view(m->qx_o, qd)));
+    } else {
+      WGD_HIP(attention_block(m, l, 1, 0, pos));
+      WGD_HIP(quantize(s, m->att, qd, nullptr, qx_view(m->qx_o, qd)));
+    }
     MVOut to_ffn;
     to_ffn.q = qx_view(m->qx_ffn, H); to_ffn.norm_w = L.ffn_norm;
     MVTarget o;
@@ -351,6 +384,11 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
   rc = rc ? rc : alloc_t(m, (uint64_t)c.context + 1, "decode tokens", &m->tokens);
   rc = rc ? rc : alloc_t(m, 2 + 2 * 256, "argmax", &m->argmax_buf);
   m->att_part_floats = attention_scratch_floats(c.heads, c.head_dim, 1, (uint32_t)device_cu_count() * 4);
+  if (decode_attention_supported(c.heads, c.kv_heads, c.head_dim))
+    for (int l = 0; l < c.layers; l++)
+      if (capacities[l] > 0)
+        m->att_part_floats = std::max(m->att_part_floats, decode_attention_scratch_floats(c.heads, c.kv_heads, c.head_dim,
+                                                                                          (uint32_t)capacities[l]));
   rc = rc ? rc : alloc_t(m, m->att_part_floats, "attention split scratch", &m->att_part);
   for (int l = 0; !rc && l < c.layers; l++) {
     if (capacities[l] < 1) { rc = fail(ctx, WGD_E_INVALID, "layer %d: KV capacity %d", l, capacities[l]); break; }
@@ -434,14 +472,14 @@ int wgd_model_tensor(wgd_model *m, const char *name, int32_t type, int32_t n_dim
   if (ne0 > 0xFFFFFFFFull || ne1 > 0xFFFFFFFFull) return fail(ctx, WGD_E_INVALID, "%s: too large", name);
   Matrix mat; mat.type = type; mat.cols = (uint32_t)ne0; mat.rows = (uint32_t)ne1;
   void *dev = nullptr;
-  int rc = alloc(m, need, label, &dev);
+  int rc = alloc(m, has_planar(type) ? planar_bytes(type, mat.cols, mat.rows) : need, label, &dev);
   if (rc) return rc;
   if (has_planar(type)) {
     void *raw = nullptr;
     rc = ctx_alloc(ctx, need, "upload staging", &raw);
     if (rc) return rc;
     rc = ctx_check(ctx, hipMemcpyAsync(raw, data, need, hipMemcpyHostToDevice, s), name);
-    if (!rc) rc = ctx_check(ctx, repack_planar(s, type, (const uint8_t *)raw, (uint8_t *)dev, need / block_bytes(type)), name);
+    if (!rc) rc = ctx_check(ctx, repack_planar(s, type, (const uint8_t *)raw, (uint8_t *)dev, mat.cols, mat.rows), name);
     if (!rc) rc = ctx_sync(ctx, name);
     ctx_free(ctx, raw);
     if (rc) return rc;
@@ -520,6 +558,24 @@ int wgd_model_ready(wgd_model *m) {
     rc = rc ? rc : alloc(m, qx_bytes(H), "qx head", &m->qx_head);
     if (rc) return rc;
     m->qpath = true;
+    const bool norms = !(is_gemma(m) || c.qk_norm) || [&] {
+      for (const Layer &L : m->L) if (!L.q_norm || !L.k_norm) return false;
+      return true;
+    }();
+    const char *fa = getenv("WGD_FUSED_ATTENTION");
+    m->fused_attention = decode_attention_supported(c.heads, c.kv_heads, c.head_dim) && norms && !(fa && fa[0] == '0');
+    if (m->fused_attention) {
+      // one table per distinct (theta, scale): the model's, and Gemma's local layers'
+      const uint32_t rot = is_gemma(m) || !c.rotary_dim ? (uint32_t)c.head_dim : (uint32_t)c.rotary_dim;
+      const uint64_t n = (uint64_t)c.context * (rot / 2);
+      rc = alloc_t(m, n * 2, "rope table", (float **)&m->rope_tab[0]);
+      if (!rc) rc = ctx_check(ctx, rope_table(ctx->stream, m->rope_tab[0], (uint32_t)c.context, rot, c.theta, c.rope_scale), "rope table");
+      if (!rc && is_gemma(m)) {
+        rc = alloc_t(m, n * 2, "rope table (local)", (float **)&m->rope_tab[1]);
+        if (!rc) rc = ctx_check(ctx, rope_table(ctx->stream, m->rope_tab[1], (uint32_t)c.context, rot, c.local_theta, 1.f), "rope table");
+      }
+      if (rc) return rc;
+    }
   }
   m->ready = true;
   return ctx_sync(ctx, "model upload");

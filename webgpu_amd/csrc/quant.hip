@@ -47,33 +47,34 @@ hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *i
 }
 
 // Gather from a planar table: element i of `row`, decoded exactly as deq_elem.
-__device__ __forceinline__ float deq_planar(int type, const uint8_t *w, uint64_t nbt, uint32_t bpr, uint32_t row, uint32_t i) {
-  const uint64_t bi = (uint64_t)row * bpr + i / block_size_dev(type);
+__device__ __forceinline__ float deq_planar(int type, const uint8_t *w, uint64_t nbp, uint32_t bpr, uint32_t cols,
+                                            uint32_t row, uint32_t i) {
   if (type == Q4_K) {
-    const uint8_t *h = w + q4_planes(nbt).hdr + bi * 16;
-    const uint32_t j = i % 256, s = j / 32, e = j % 32;
+    const uint8_t *h = w + q4_planes(nbp).hdr + tiled(row, i / 256, bpr) * 16;
+    const uint32_t j = i % 256, s = j / 32;
     uint32_t sc, mn;
     if (s < 4) { sc = h[4 + s] & 63u; mn = h[8 + s] & 63u; }
     else { sc = (h[8 + s] & 15u) | ((h[s] >> 6) << 4); mn = (h[8 + s] >> 4) | ((h[4 + s] >> 6) << 4); }
-    const uint32_t q = q4_quant(w, bi * 8 + s, e);
+    const uint32_t q = q4_quant(w, row, cols / 32, i);
     return half_bits(h[0] | ((uint32_t)h[1] << 8)) * (float)(sc * q) - half_bits(h[2] | ((uint32_t)h[3] << 8)) * (float)mn;
   }
   if (type == Q6_K) {
-    const Q6Planes p = q6_planes(nbt);
-    const uint32_t j = i % 256, s = j / 32, e = j % 32;
-    const uint64_t ci = bi * 8 + s;
-    const float sc = (float)(int8_t)w[p.sc + ci * 2 + e / 16];
-    return half_bits(w[p.d + bi * 2] | ((uint32_t)w[p.d + bi * 2 + 1] << 8)) * sc * (float)((int)q6_quant(w, nbt, ci, e) - 32);
+    const Q6Planes p = q6_planes(nbp);
+    const uint32_t C = cols / 32;
+    const float sc = (float)(int8_t)w[p.sc + tiled(row, i / 32, C) * 2 + (i % 32) / 16];
+    const uint64_t d = p.d + tiled(row, i / 256, bpr) * 2;
+    return half_bits(w[d] | ((uint32_t)w[d + 1] << 8)) * sc * (float)((int)q6_quant(w, nbp, row, C, i) - 32);
   }
-  const Q8Planes p = q8_planes(nbt);
-  return half_bits(w[p.d + bi * 2] | ((uint32_t)w[p.d + bi * 2 + 1] << 8)) * (float)(int8_t)w[p.qs + bi * 32 + i % 32];
+  const Q8Planes p = q8_planes(nbp);
+  const uint64_t d = p.d + tiled(row, i / 32, bpr) * 2;
+  return half_bits(w[d] | ((uint32_t)w[d + 1] << 8)) * (float)(int8_t)w[p.qs + tiled(row, i / 16, cols / 16) * 16 + i % 16];
 }
 
-__global__ void k_embed_planar(int type, const uint8_t *table, uint64_t nbt, uint32_t bpr, const int32_t *ids, float *out,
+__global__ void k_embed_planar(int type, const uint8_t *table, uint64_t nbp, uint32_t bpr, const int32_t *ids, float *out,
                                uint32_t hidden, double scale) {
   uint32_t b = blockIdx.y, row = (uint32_t)ids[b];
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
-    float v = deq_planar(type, table, nbt, bpr, row, i);
+    float v = deq_planar(type, table, nbp, bpr, hidden, row, i);
     out[(uint64_t)b * hidden + i] = scale == 1.0 ? v : (float)((double)v * scale);
   }
 }
@@ -83,8 +84,8 @@ hipError_t embed_matrix(hipStream_t s, const Matrix &t, const int32_t *ids, floa
   if (!n) return hipSuccess;
   uint32_t gx = (t.cols + 255) / 256; if (gx > 64) gx = 64;
   uint32_t bpr = t.cols / block_size(t.type);
-  hipLaunchKernelGGL(k_embed_planar, dim3(gx, n), dim3(256), 0, s, t.type, t.data, (uint64_t)bpr * t.rows, bpr, ids, out,
-                     t.cols, scale);
+  hipLaunchKernelGGL(k_embed_planar, dim3(gx, n), dim3(256), 0, s, t.type, t.data, (uint64_t)bpr * tile_rows(t.rows), bpr,
+                     ids, out, t.cols, scale);
   return hipGetLastError();
 }
 
@@ -92,65 +93,89 @@ hipError_t embed_matrix(hipStream_t s, const Matrix &t, const int32_t *ids, floa
 
 bool has_planar(int type) { return type == Q4_K || type == Q6_K || type == Q8_0; }
 
-// One thread per block. Q4_K: chunk j (sub-block j) byte i = q[32j + i] | q[32j + 16 + i] << 4,
-// with q[e] the GGUF quant of element e (byte 16 + 32*(e/64) + e%32, nibble (e%64)/32).
-__global__ void k_repack_q4(const uint8_t *src, uint8_t *dst, uint64_t nb) {
-  const Q4Planes p = q4_planes(nb);
+uint64_t planar_bytes(int type, uint32_t cols, uint32_t rows) { return tile_rows(rows) * row_bytes(type, cols); }
+
+// One thread per GGUF block (row, b). Q4_K: chunk c = 8b + j byte i = q[32j + i] | q[32j + 16 + i]
+// << 4, with q[e] the block's quant of element e (byte 16 + 32*(e/64) + e%32, nibble
+// (e%64)/32); the 16-byte header copied.
+__global__ void k_repack_q4(const uint8_t *src, uint8_t *dst, uint32_t bpr, uint32_t rows) {
+  const uint64_t nb = (uint64_t)rows * bpr, nbp = tile_rows(rows) * bpr;
+  const uint32_t C = bpr * 8;
+  const Q4Planes p = q4_planes(nbp);
   for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
-    const uint8_t *b = src + blk * 144;
-    for (int o = 0; o < 16; o++) dst[p.hdr + blk * 16 + o] = b[o];
-    auto q = [&](uint32_t e) -> uint32_t { return (b[16 + 32 * (e / 64) + e % 32] >> (4 * ((e % 64) / 32))) & 15u; };
-    for (uint32_t j = 0; j < 8; j++)
-      for (uint32_t i = 0; i < 16; i++) dst[p.qs + blk * 128 + 16 * j + i] = (uint8_t)(q(32 * j + i) | (q(32 * j + 16 + i) << 4));
+    const uint32_t row = (uint32_t)(blk / bpr), b = (uint32_t)(blk % bpr);
+    const uint8_t *s = src + blk * 144;
+    uint8_t *h = dst + p.hdr + tiled(row, b, bpr) * 16;
+    for (int o = 0; o < 16; o++) h[o] = s[o];
+    auto q = [&](uint32_t e) -> uint32_t { return (s[16 + 32 * (e / 64) + e % 32] >> (4 * ((e % 64) / 32))) & 15u; };
+    for (uint32_t j = 0; j < 8; j++) {
+      uint8_t *c = dst + p.qs + tiled(row, 8 * b + j, C) * 16;
+      for (uint32_t i = 0; i < 16; i++) c[i] = (uint8_t)(q(32 * j + i) | (q(32 * j + 16 + i) << 4));
+    }
   }
 }
 
-// Q6_K: ql chunk j byte i = lo4[32j + i] | lo4[32j + 16 + i] << 4; qh chunk j dword m byte b =
-// hi2 of elements 32j + {8m+b, 16+8m+b, 8m+4+b, 16+8m+4+b} at bits 0, 2, 4, 6; scales and d
-// copied (GGUF element e: lo4 from ql[64(e/128) + 32((e%128/32)&1) + e%32] >> 4((e%128/32)>>1),
+// Q6_K: ql chunk byte i = lo4[32j + i] | lo4[32j + 16 + i] << 4; qh chunk dword m byte b = hi2 of
+// elements 32j + {8m+b, 16+8m+b, 8m+4+b, 16+8m+4+b} at bits 0, 2, 4, 6; the chunk's two scales;
+// d per block (GGUF element e: lo4 from ql[64(e/128) + 32((e%128/32)&1) + e%32] >> 4((e%128/32)>>1),
 // hi2 from qh[32(e/128) + e%32] >> 2(e%128/32)).
-__global__ void k_repack_q6(const uint8_t *src, uint8_t *dst, uint64_t nb) {
-  const Q6Planes p = q6_planes(nb);
+__global__ void k_repack_q6(const uint8_t *src, uint8_t *dst, uint32_t bpr, uint32_t rows) {
+  const uint64_t nb = (uint64_t)rows * bpr, nbp = tile_rows(rows) * bpr;
+  const uint32_t C = bpr * 8;
+  const Q6Planes p = q6_planes(nbp);
   for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
-    const uint8_t *b = src + blk * 210;
+    const uint32_t row = (uint32_t)(blk / bpr), b = (uint32_t)(blk % bpr);
+    const uint8_t *s = src + blk * 210;
     auto lo4 = [&](uint32_t e) -> uint32_t {
       const uint32_t h = e / 128, t = (e % 128) / 32, l = e % 32;
-      return (b[64 * h + 32 * (t & 1) + l] >> (4 * (t >> 1))) & 15u;
+      return (s[64 * h + 32 * (t & 1) + l] >> (4 * (t >> 1))) & 15u;
     };
     auto hi2 = [&](uint32_t e) -> uint32_t {
       const uint32_t h = e / 128, t = (e % 128) / 32, l = e % 32;
-      return (b[128 + 32 * h + l] >> (2 * t)) & 3u;
+      return (s[128 + 32 * h + l] >> (2 * t)) & 3u;
     };
     for (uint32_t j = 0; j < 8; j++) {
-      for (uint32_t i = 0; i < 16; i++) dst[p.ql + blk * 128 + 16 * j + i] = (uint8_t)(lo4(32 * j + i) | (lo4(32 * j + 16 + i) << 4));
+      const uint64_t ci = tiled(row, 8 * b + j, C);
+      for (uint32_t i = 0; i < 16; i++) dst[p.ql + ci * 16 + i] = (uint8_t)(lo4(32 * j + i) | (lo4(32 * j + 16 + i) << 4));
       for (uint32_t m = 0; m < 2; m++)
         for (uint32_t bb = 0; bb < 4; bb++) {
           const uint32_t e = 32 * j + 8 * m + bb;
-          dst[p.qh + blk * 64 + 8 * j + 4 * m + bb] =
-              (uint8_t)(hi2(e) | (hi2(e + 16) << 2) | (hi2(e + 4) << 4) | (hi2(e + 20) << 6));
+          dst[p.qh + ci * 8 + 4 * m + bb] = (uint8_t)(hi2(e) | (hi2(e + 16) << 2) | (hi2(e + 4) << 4) | (hi2(e + 20) << 6));
         }
+      dst[p.sc + ci * 2] = s[192 + 2 * j];
+      dst[p.sc + ci * 2 + 1] = s[192 + 2 * j + 1];
     }
-    for (int o = 0; o < 16; o++) dst[p.sc + blk * 16 + o] = b[192 + o];
-    dst[p.d + blk * 2] = b[208];
-    dst[p.d + blk * 2 + 1] = b[209];
-  }
-}
-__global__ void k_repack_q8(const uint8_t *src, uint8_t *dst, uint64_t nb) {
-  Q8Planes p = q8_planes(nb);
-  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nb * 34; i += (uint64_t)gridDim.x * blockDim.x) {
-    uint64_t blk = i / 34; uint32_t o = i % 34; uint8_t v = src[i];
-    if (o < 2) dst[p.d + blk * 2 + o] = v; else dst[p.qs + blk * 32 + (o - 2)] = v;
+    const uint64_t d = p.d + tiled(row, b, bpr) * 2;
+    dst[d] = s[208];
+    dst[d + 1] = s[209];
   }
 }
 
-hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint64_t blocks) {
-  if (!blocks) return hipSuccess;
-  uint64_t bytes = blocks * block_bytes(type), grid = (bytes + 255) / 256; if (grid > 65535 * 8) grid = 65535 * 8;
-  if (type != Q8_0) { grid = (blocks + 255) / 256; if (grid > 65535 * 8) grid = 65535 * 8; }
-  if (type == Q4_K) hipLaunchKernelGGL(k_repack_q4, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, blocks);
-  else if (type == Q6_K) hipLaunchKernelGGL(k_repack_q6, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, blocks);
-  else if (type == Q8_0) hipLaunchKernelGGL(k_repack_q8, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, blocks);
-  else return hipErrorInvalidValue;
+// Q8_0: the 32 quants as two 16-element chunks, d per block.
+__global__ void k_repack_q8(const uint8_t *src, uint8_t *dst, uint32_t bpr, uint32_t rows) {
+  const uint64_t nb = (uint64_t)rows * bpr, nbp = tile_rows(rows) * bpr;
+  const uint32_t C = bpr * 2;
+  const Q8Planes p = q8_planes(nbp);
+  for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t row = (uint32_t)(blk / bpr), b = (uint32_t)(blk % bpr);
+    const uint8_t *s = src + blk * 34;
+    const uint64_t d = p.d + tiled(row, b, bpr) * 2;
+    dst[d] = s[0];
+    dst[d + 1] = s[1];
+    for (uint32_t h = 0; h < 2; h++)
+      for (uint32_t i = 0; i < 16; i++) dst[p.qs + tiled(row, 2 * b + h, C) * 16 + i] = s[2 + 16 * h + i];
+  }
+}
+
+hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint32_t cols, uint32_t rows) {
+  if (!rows || !cols) return hipSuccess;
+  if (!has_planar(type) || cols % block_size(type)) return hipErrorInvalidValue;
+  const uint32_t bpr = cols / block_size(type);
+  uint64_t grid = ((uint64_t)rows * bpr + 255) / 256;
+  if (grid > 65535 * 8) grid = 65535 * 8;
+  if (type == Q4_K) hipLaunchKernelGGL(k_repack_q4, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
+  else if (type == Q6_K) hipLaunchKernelGGL(k_repack_q6, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
+  else hipLaunchKernelGGL(k_repack_q8, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
   return hipGetLastError();
 }
 

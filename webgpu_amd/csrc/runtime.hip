@@ -180,13 +180,13 @@ int wgd_upload_weights(wgd_context *ctx, int32_t type, uint32_t cols, uint32_t r
   uint64_t need = (uint64_t)rows * row_bytes(type, cols);
   if (bytes != need) return fail(ctx, WGD_E_INVALID, "wgd_upload_weights: %llu bytes given, shape needs %llu", (unsigned long long)bytes, (unsigned long long)need);
   wgd_buffer *b = nullptr;
-  int rc = wgd_buffer_create(ctx, need, label ? label : "weights", &b);
+  int rc = wgd_buffer_create(ctx, has_planar(type) ? planar_bytes(type, cols, rows) : need, label ? label : "weights", &b);
   if (rc) return rc;
   if (has_planar(type)) {
     void *raw = nullptr;
     rc = ctx_alloc(ctx, need, "upload staging", &raw);
     if (!rc) rc = ctx_check(ctx, hipMemcpyAsync(raw, data, need, hipMemcpyHostToDevice, ctx->stream), "wgd_upload_weights");
-    if (!rc) rc = ctx_check(ctx, repack_planar(ctx->stream, type, (const uint8_t *)raw, (uint8_t *)b->ptr, need / block_bytes(type)), "wgd_upload_weights");
+    if (!rc) rc = ctx_check(ctx, repack_planar(ctx->stream, type, (const uint8_t *)raw, (uint8_t *)b->ptr, cols, rows), "wgd_upload_weights");
     if (!rc) rc = ctx_sync(ctx, "wgd_upload_weights");
     ctx_free(ctx, raw);
     b->layout = LAYOUT_PLANAR;
