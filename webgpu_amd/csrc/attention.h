@@ -19,8 +19,7 @@ struct DecodeAttnArgs {
   float *y;
   QXOut qx;
   const int32_t *pos;
-  const float2 *rope_table;      // (cos, sin) per position and rotation pair, or null
-  uint32_t rope_positions;       // positions the table covers
+  const double *inv_freq;        // theta^(-2i/rot) per rotation pair (rope_inv_freq)
   uint32_t heads, kv_heads, hd, rot, capacity, window;
   float scale, theta, rope_scale, eps;
   int mode;
@@ -28,8 +27,8 @@ struct DecodeAttnArgs {
 bool decode_attention_supported(uint32_t heads, uint32_t kv_heads, uint32_t hd);
 uint64_t decode_attention_scratch_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t capacity);
 hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &a);
-// tab[p * (rot/2) + i] = (cos, sin) of p * scale * theta^(-2i/rot), the angle formed in f64
-// as in wgd::rope, for p < positions.
-hipError_t rope_table(hipStream_t s, float2 *tab, uint32_t positions, uint32_t rot, float theta, float scale);
+// f[i] = theta^(-2i/rot) in f64 for i < rot/2: the rotation angle of pair i at position p is
+// p * scale * f[i], formed in f64 as in wgd::rope.
+hipError_t rope_inv_freq(hipStream_t s, double *f, uint32_t rot, float theta);
 
 }  // namespace wgd

@@ -245,7 +245,8 @@ constexpr uint32_t AD_WAVES = 4;
 struct AttnDecK {
   const float *q, *k, *v; float *kc, *vc; const float *qn, *kn; float *part;
   const int32_t *pos;
-  const float2 *tab; uint32_t tab_pos;
+  const double *invf;
+
   uint32_t heads, kvh, rot, cap, window, group, chunk, nsplit;
   float scale, theta, rscale, eps; int mode;
 };
@@ -282,17 +283,11 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
   // ---- prologue: Q/K norm and RoPE of the group's query heads and the new key
   const uint32_t half = a.rot / 2;
   for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
-    if (a.tab && pos < a.tab_pos) {
-      const float2 cs = a.tab[(uint64_t)pos * half + i];
-      csn[2 * i] = cs.x;
-      csn[2 * i + 1] = cs.y;
-    } else {
-      const double angle = (double)pos * (double)a.rscale * pow((double)a.theta, -(double)(2 * i) / (double)a.rot);
-      double sd, cd;
-      sincos(angle, &sd, &cd);
-      csn[2 * i] = (float)cd;
-      csn[2 * i + 1] = (float)sd;
-    }
+    const double angle = (double)pos * (double)a.rscale * a.invf[i];
+    double sd, cd;
+    sincos(angle, &sd, &cd);
+    csn[2 * i] = (float)cd;
+    csn[2 * i + 1] = (float)sd;
   }
   for (uint32_t it = w; it <= g; it += AD_WAVES) {
     const bool isk = it == g;
@@ -411,10 +406,172 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
   }
 }
 
+// The same step with everything a lane needs kept in registers: lane l holds elements
+// l + 64e of a head (half-split rotation, rot == hd: pair (i, i + hd/2) sits in one lane) or
+// EL*l + e (adjacent pairs). The projections, norm weights and rotation frequencies are
+// loaded before the position is known; the angles are formed in f64 (p * scale * f[i]) as in
+// k_rope. Each wavefront rotates the query heads itself, so no barrier precedes the keys.
+template <int EL, int G, bool ADJ>
+__global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
+  constexpr uint32_t HD = 64 * EL, NP = EL / 2;
+  __shared__ float wm[AD_WAVES][G], wl[AD_WAVES][G];
+  __shared__ float wo[AD_WAVES][G][HD];
+  const uint32_t lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t kv = blockIdx.x, z = blockIdx.y, g = a.group;
+  auto el = [&](int e) -> uint32_t { return ADJ ? EL * lane + e : lane + 64 * e; };
+  // ---- loads that do not depend on the position
+  float q[G][EL], kn[EL], vn[EL], qw[EL], kw[EL];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int e = 0; e < EL; e++) q[i][e] = (uint32_t)i < g ? a.q[((uint64_t)kv * g + i) * HD + el(e)] : 0.f;
+#pragma unroll
+  for (int e = 0; e < EL; e++) {
+    kn[e] = a.k[(uint64_t)kv * HD + el(e)];
+    vn[e] = a.v[(uint64_t)kv * HD + el(e)];
+    qw[e] = a.mode == 0 ? a.qn[el(e)] : 1.f;
+    kw[e] = a.mode == 0 ? a.kn[el(e)] : 1.f;
+  }
+  double f[NP];
+#pragma unroll
+  for (int e = 0; e < (int)NP; e++) f[e] = a.invf[ADJ ? NP * lane + e : lane + 64 * e];
+  const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane(*a.pos);
+  const uint32_t end = pos + 1, win = end < a.window ? end : a.window, begin = end - win;
+  const uint32_t lo = begin + z * a.chunk;
+  if (lo >= end) return;
+  const uint32_t hi = lo + a.chunk < end ? lo + a.chunk : end;
+  const uint32_t nb = a.chunk / (AD_WAVES * AD_KPB);
+  const uint64_t rowf = (uint64_t)a.kvh * HD;
+  float kr[AD_KPB][EL], vr[AD_KPB][EL];
+  auto load_batch = [&](uint32_t b) {
+#pragma unroll
+    for (uint32_t k = 0; k < AD_KPB; k++) {
+      uint32_t t = lo + (b * AD_WAVES + w) * AD_KPB + k;
+      if (t >= hi) t = lo;
+      const uint64_t base = (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD;
+#pragma unroll
+      for (int e = 0; e < EL; e++) { kr[k][e] = a.kc[base + el(e)]; vr[k][e] = a.vc[base + el(e)]; }
+    }
+  };
+  load_batch(0);
+  // ---- Q/K norm and rotation in registers
+  if (a.mode == 0) {
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < EL; e++) ss += q[i][e] * q[i][e];
+      const float inv = 1.f / sqrtf(wave_total(ss) / (float)HD + a.eps);
+#pragma unroll
+      for (int e = 0; e < EL; e++) q[i][e] = q[i][e] * qw[e] * inv;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EL; e++) ss += kn[e] * kn[e];
+    const float inv = 1.f / sqrtf(wave_total(ss) / (float)HD + a.eps);
+#pragma unroll
+    for (int e = 0; e < EL; e++) kn[e] = kn[e] * kw[e] * inv;
+  }
+#pragma unroll
+  for (int e = 0; e < (int)NP; e++) {
+    double sd, cd;
+    sincos((double)pos * (double)a.rscale * f[e], &sd, &cd);
+    const float c = (float)cd, sn = (float)sd;
+    const int ia = ADJ ? 2 * e : e, ib = ADJ ? 2 * e + 1 : e + (int)NP;
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const float xa = q[i][ia], xb = q[i][ib];
+      q[i][ia] = xa * c - xb * sn;
+      q[i][ib] = xa * sn + xb * c;
+    }
+    const float xa = kn[ia], xb = kn[ib];
+    kn[ia] = xa * c - xb * sn;
+    kn[ib] = xa * sn + xb * c;
+  }
+  if (pos >= lo && pos < hi && w == 0) {
+    const uint64_t slot = (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
+#pragma unroll
+    for (int e = 0; e < EL; e++) { a.kc[slot + el(e)] = kn[e]; a.vc[slot + el(e)] = vn[e]; }
+  }
+  // ---- keys
+  float m[G], l[G], o[G][EL];
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    m[i] = -INFINITY; l[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EL; e++) o[i][e] = 0.f;
+  }
+  for (uint32_t b = 0; b < nb; b++) {
+    if (b > 0) load_batch(b);
+    const uint32_t t0 = lo + (b * AD_WAVES + w) * AD_KPB;
+    if (t0 >= hi) break;  // uniform: later batches of this wavefront are past the chunk too
+    float sc[AD_KPB][G];
+#pragma unroll
+    for (uint32_t k = 0; k < AD_KPB; k++) {
+      if (t0 + k == pos) {
+#pragma unroll
+        for (int e = 0; e < EL; e++) { kr[k][e] = kn[e]; vr[k][e] = vn[e]; }
+      }
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < EL; e++) d += q[i][e] * kr[k][e];
+        sc[k][i] = t0 + k < hi ? wave_total(d) * a.scale : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      float bm = sc[0][i];
+#pragma unroll
+      for (uint32_t k = 1; k < AD_KPB; k++) bm = fmaxf(bm, sc[k][i]);
+      const float mn = fmaxf(m[i], bm);  // finite: key t0 is inside the chunk
+      const float corr = m[i] == -INFINITY ? 0.f : expf(m[i] - mn);
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < EL; e++) o[i][e] *= corr;
+#pragma unroll
+      for (uint32_t k = 0; k < AD_KPB; k++) {
+        const float p = sc[k][i] == -INFINITY ? 0.f : expf(sc[k][i] - mn);
+        ps += p;
+#pragma unroll
+        for (int e = 0; e < EL; e++) o[i][e] += p * vr[k][e];
+      }
+      l[i] = l[i] * corr + ps;
+      m[i] = mn;
+    }
+  }
+  // ---- merge the wavefronts
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    if (lane == 0) { wm[w][i] = m[i]; wl[w][i] = l[i]; }
+#pragma unroll
+    for (int e = 0; e < EL; e++) wo[w][i][el(e)] = o[i][e];
+  }
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < g * HD; j += blockDim.x) {
+    const uint32_t i = j / HD, d = j % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) M = fmaxf(M, wm[u][i]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) {
+      if (wm[u][i] == -INFINITY) continue;
+      const float fz = expf(wm[u][i] - M);
+      L += wl[u][i] * fz;
+      O += wo[u][i][d] * fz;
+    }
+    float *pp = a.part + (((uint64_t)kv * g + i) * a.nsplit + z) * (HD + 2);
+    if (d == 0) { pp[0] = M; pp[1] = L; }
+    pp[2 + d] = O;
+  }
+}
+
 // Merge of the chunks of one query head: thread d owns output element d. The partials were
-// written by the previous launch (other XCDs' L2), so every load is issued before any is
-// used: one round trip for the (max, sum) pairs, one per 16 chunks for the outputs.
-constexpr uint32_t AD_MAX_SPLITS = 1024;
+// written by the previous launch (other XCDs' L2): after the position, every load goes out
+// at once (the first AD_ZB chunks' outputs in registers), so the merge is one round trip.
+constexpr uint32_t AD_MAX_SPLITS = 1024, AD_ZB = 32;
 __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, QXOut qx, const int32_t *pos_dev,
                                                    uint32_t window, uint32_t chunk, uint32_t nsplit, uint32_t hd) {
   __shared__ float wz[AD_MAX_SPLITS];
@@ -424,11 +581,12 @@ __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, 
   const uint32_t end = pos + 1, win = end < window ? end : window;
   const uint32_t nact = (win + chunk - 1) / chunk;
   const float *pp = part + (uint64_t)h * nsplit * (hd + 2);
-  // (max, sum) of chunk z in thread z
+  float ov[AD_ZB];
+#pragma unroll
+  for (uint32_t k = 0; k < AD_ZB; k++) ov[k] = k < nact && d < hd ? pp[(uint64_t)k * (hd + 2) + 2 + d] : 0.f;
   float mz = -INFINITY, lz = 0.f;
-  for (uint32_t z = d; z < nact; z += blockDim.x) {
-    mz = fmaxf(mz, pp[(uint64_t)z * (hd + 2)]);
-  }
+  if (d < nact) { mz = pp[(uint64_t)d * (hd + 2)]; lz = pp[(uint64_t)d * (hd + 2) + 1]; }
+  for (uint32_t zz = d + blockDim.x; zz < nact; zz += blockDim.x) mz = fmaxf(mz, pp[(uint64_t)zz * (hd + 2)]);
   float M = mz;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
@@ -437,51 +595,36 @@ __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, 
   M = red[0];
   for (uint32_t u = 1; u < nw; u++) M = fmaxf(M, red[u]);
   float L = 0.f;
-  for (uint32_t z = d; z < nact; z += blockDim.x) {
-    const float f = expf(pp[(uint64_t)z * (hd + 2)] - M);
-    wz[z] = f;
-    lz += pp[(uint64_t)z * (hd + 2) + 1] * f;
+  if (d < nact) { const float f = expf(mz - M); wz[d] = f; L = lz * f; }
+  for (uint32_t zz = d + blockDim.x; zz < nact; zz += blockDim.x) {
+    const float f = expf(pp[(uint64_t)zz * (hd + 2)] - M);
+    wz[zz] = f;
+    L += pp[(uint64_t)zz * (hd + 2) + 1] * f;
   }
-  L = wave_sum(lz);
+  L = wave_sum(L);
   __syncthreads();
   if (lane == 0) red[wv] = L;
   __syncthreads();
   L = 0.f;
   for (uint32_t u = 0; u < nw; u++) L += red[u];
   float O = 0.f;
-  if (d < hd) {
-    uint32_t z = 0;
-    for (; z + 16 <= nact; z += 16) {
-      float v[16];
 #pragma unroll
-      for (int k = 0; k < 16; k++) v[k] = pp[(uint64_t)(z + k) * (hd + 2) + 2 + d];
-#pragma unroll
-      for (int k = 0; k < 16; k++) O += v[k] * wz[z + k];
-    }
-    for (; z < nact; z++) O += pp[(uint64_t)z * (hd + 2) + 2 + d] * wz[z];
-  }
+  for (uint32_t k = 0; k < AD_ZB; k++) if (k < nact) O += ov[k] * wz[k];
+  if (d < hd)
+    for (uint32_t k = AD_ZB; k < nact; k++) O += pp[(uint64_t)k * (hd + 2) + 2 + d] * wz[k];
   const float out = O / L;
   if (d < hd) y[(uint64_t)h * hd + d] = out;
   if (qx.d0) qx_store(qx, h * hd + d, out, out, d < hd);
 }
 
-__global__ void k_rope_table(float2 *tab, uint32_t positions, uint32_t half, uint32_t rot, float theta, float scale) {
-  const uint64_t n = (uint64_t)positions * half;
-  for (uint64_t j = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; j < n; j += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t p = (uint32_t)(j / half), i = (uint32_t)(j % half);
-    const double angle = (double)p * (double)scale * pow((double)theta, -(double)(2 * i) / (double)rot);
-    double sd, cd;
-    sincos(angle, &sd, &cd);
-    tab[j] = make_float2((float)cd, (float)sd);
-  }
+__global__ void k_inv_freq(double *f, uint32_t half, uint32_t rot, float theta) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < half; i += gridDim.x * blockDim.x)
+    f[i] = pow((double)theta, -(double)(2 * i) / (double)rot);
 }
 
-hipError_t rope_table(hipStream_t s, float2 *tab, uint32_t positions, uint32_t rot, float theta, float scale) {
-  if (!positions || rot < 2 || rot % 2) return hipErrorInvalidValue;
-  const uint64_t n = (uint64_t)positions * (rot / 2);
-  uint64_t grid = (n + 255) / 256;
-  if (grid > 65535) grid = 65535;
-  hipLaunchKernelGGL(k_rope_table, dim3((uint32_t)grid), dim3(256), 0, s, tab, positions, rot / 2, rot, theta, scale);
+hipError_t rope_inv_freq(hipStream_t s, double *f, uint32_t rot, float theta) {
+  if (rot < 2 || rot % 2) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_inv_freq, dim3((rot / 2 + 255) / 256), dim3(256), 0, s, f, rot / 2, rot, theta);
   return hipGetLastError();
 }
 
@@ -504,6 +647,20 @@ uint64_t decode_attention_scratch_floats(uint32_t heads, uint32_t kv_heads, uint
 
 template <int EL>
 static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
+  // registers only: full-width rotation with its pairs inside a lane (EL >= 2)
+  const bool fast = EL >= 2 && (k.mode == 2 || k.rot == 64u * EL);
+  if (fast) {
+    constexpr int E = EL >= 2 ? EL : 2;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, k); };
+    if (k.mode == 2) {
+      if (k.group <= 1) go(k_attn_fast<E, 1, true>); else if (k.group <= 2) go(k_attn_fast<E, 2, true>);
+      else if (k.group <= 4) go(k_attn_fast<E, 4, true>); else go(k_attn_fast<E, 8, true>);
+    } else {
+      if (k.group <= 1) go(k_attn_fast<E, 1, false>); else if (k.group <= 2) go(k_attn_fast<E, 2, false>);
+      else if (k.group <= 4) go(k_attn_fast<E, 4, false>); else go(k_attn_fast<E, 8, false>);
+    }
+    return;
+  }
   if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec<EL, 1>), grid, dim3(256), 0, s, k);
   else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec<EL, 2>), grid, dim3(256), 0, s, k);
   else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec<EL, 4>), grid, dim3(256), 0, s, k);
@@ -512,11 +669,11 @@ static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
 
 hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
   if (!decode_attention_supported(in.heads, in.kv_heads, in.hd) || !in.capacity || !in.window || !in.pos ||
-      !in.partial || (in.mode == 0 && (!in.q_norm || !in.k_norm)) || in.rot > in.hd || in.rot % 2)
+      !in.partial || !in.inv_freq || (in.mode == 0 && (!in.q_norm || !in.k_norm)) || in.rot > in.hd || in.rot % 2)
     return hipErrorInvalidValue;
   AttnDecK k;
   k.q = in.q; k.k = in.k; k.v = in.v; k.kc = in.kc; k.vc = in.vc; k.qn = in.q_norm; k.kn = in.k_norm;
-  k.part = in.partial; k.pos = in.pos; k.tab = in.rope_table; k.tab_pos = in.rope_table ? in.rope_positions : 0;
+  k.part = in.partial; k.pos = in.pos; k.invf = in.inv_freq;
   k.heads = in.heads; k.kvh = in.kv_heads; k.rot = in.rot ? in.rot : in.hd; k.cap = in.capacity;
   k.window = in.window; k.group = in.heads / in.kv_heads;
   k.chunk = dec_chunk(in.capacity, in.kv_heads);

@@ -71,8 +71,8 @@ struct MVOut {
   const float *norm_w = nullptr;
 };
 
-// One matrix of a launch. Several matrices of one type that read the same activation
-// (the Q and K projections) run in one launch, one row-tile range each.
+// One matrix of a launch. Several matrices that read the same activation (the Q, K and V
+// projections) run in one launch, one row-tile range each: of one type, or Q4_K and Q6_K.
 struct MVTarget {
   const Matrix *w = nullptr;
   const Matrix *w1 = nullptr;  // the up matrix of a gated pair (MV_SILU / MV_GELU)
@@ -93,6 +93,7 @@ struct MVSeg {
   uint32_t nbp;        // blocks of the padded matrix (plane offsets)
   uint32_t bpr;        // blocks per row
   uint32_t rows, tiles;
+  uint32_t kind;       // chunk type: 0 the launch's first, 1 the other K-quant
   float *y;
   const float *bias;
 };

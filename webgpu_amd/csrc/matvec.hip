@@ -28,6 +28,7 @@
 // workgroups inside a launch: on MI355X each XCD has its own L2, and device-scope fences
 // write back and invalidate it.
 #include <cstdlib>
+#include <type_traits>
 
 #include "internal.h"
 #include "decode.h"
@@ -224,21 +225,13 @@ __host__ __device__ inline LdsMap lds_map(uint32_t ke, uint32_t ns, uint32_t rt,
   return l;
 }
 
+// The body of one workgroup: row tile t of segment g, weights of chunk type T.
 template <class T, int DU, bool GLU>
-__global__ __launch_bounds__(1024) void k_mv(MV m) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+__device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t, uint8_t *lds) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t s = wv % m.NS, rg = wv / m.NS;
   const LdsMap L = lds_map(m.ke, m.NS, m.RT, GLU);
-  // segment of this workgroup (uniform)
-  uint32_t t = blockIdx.x;
-  MVSeg g = m.seg[0];
-  if (m.nseg > 1 && t >= m.seg[0].tiles) {
-    t -= m.seg[0].tiles;
-    g = m.seg[1];
-    if (m.nseg > 2 && t >= m.seg[1].tiles) { t -= m.seg[1].tiles; g = m.seg[2]; }
-  }
   const Rsrc rw = make_rsrc(g.w, g.bytes);
   const Rsrc rw1 = make_rsrc(GLU ? g.w1 : g.w, g.bytes);
   const uint32_t row0 = t * m.RT, tile0 = row0 / 16;
@@ -380,6 +373,24 @@ __global__ __launch_bounds__(1024) void k_mv(MV m) {
   finish_row(m, g, row0 + row, inside, v * xm, v1 * xm);
 }
 
+// One workgroup per row tile. T1 is the chunk type of segments with kind 1 (Q and K in
+// Q4_K with V in Q6_K run as one launch); both types have 32-element chunks.
+template <class T0, class T1, int DU, bool GLU>
+__global__ __launch_bounds__(1024) void k_mv(MV m) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // segment of this workgroup (uniform)
+  uint32_t t = blockIdx.x;
+  MVSeg g = m.seg[0];
+  if (m.nseg > 1 && t >= m.seg[0].tiles) {
+    t -= m.seg[0].tiles;
+    g = m.seg[1];
+    if (m.nseg > 2 && t >= m.seg[1].tiles) { t -= m.seg[1].tiles; g = m.seg[2]; }
+  }
+  if constexpr (std::is_same<T0, T1>::value) mv_tile<T0, DU, GLU>(m, g, t, lds);
+  else if (g.kind == 0) mv_tile<T0, DU, GLU>(m, g, t, lds);
+  else mv_tile<T1, DU, GLU>(m, g, t, lds);
+}
+
 // ------------------------------------------------------------------ host side
 
 uint64_t qx_bytes(uint32_t K) {
@@ -482,7 +493,7 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
   return best_p;
 }
 
-template <class T, bool GLU>
+template <class T0, class T1, bool GLU>
 static hipError_t launch_t(hipStream_t s, const MV &m, const MVPlan &p) {
   const dim3 grid(p.tiles), block(p.threads);
   auto go = [&](auto kernel) -> hipError_t {
@@ -495,10 +506,10 @@ static hipError_t launch_t(hipStream_t s, const MV &m, const MVPlan &p) {
     return hipGetLastError();
   };
   switch (p.DU) {
-    case 1: return go(k_mv<T, 1, GLU>);
-    case 2: return go(k_mv<T, 2, GLU>);
-    case 4: return go(k_mv<T, 4, GLU>);
-    case 8: if constexpr (!GLU) return go(k_mv<T, 8, GLU>); else break;
+    case 1: return go(k_mv<T0, T1, 1, GLU>);
+    case 2: return go(k_mv<T0, T1, 2, GLU>);
+    case 4: return go(k_mv<T0, T1, 4, GLU>);
+    case 8: if constexpr (!GLU) return go(k_mv<T0, T1, 8, GLU>); else break;
   }
   return hipErrorInvalidValue;
 }
@@ -512,9 +523,16 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   if ((epi == MV_SILU || epi == MV_GELU) != glu) return hipErrorInvalidValue;
   if (x.len != w0.cols) return hipErrorInvalidValue;
   uint32_t rows[MV_MAX_SEGS];
+  // Q4_K and Q6_K segments may share a launch (same chunk shape); other types run alone
+  const bool kq0 = w0.type == Q4_K || w0.type == Q6_K;
+  int other = -1;
   for (uint32_t i = 0; i < n; i++) {
     const Matrix &w = *t[i].w;
-    if (!mv_supported(w) || w.type != w0.type || w.cols != w0.cols || !t[i].y) return hipErrorInvalidValue;
+    if (w.type != w0.type) {
+      if (!kq0 || !(w.type == Q4_K || w.type == Q6_K) || glu) return hipErrorInvalidValue;
+      other = w.type;
+    }
+    if (!mv_supported(w) || w.cols != w0.cols || !t[i].y) return hipErrorInvalidValue;
     if ((t[i].w1 != nullptr) != glu) return hipErrorInvalidValue;
     if (glu) {
       const Matrix &w1 = *t[i].w1;
@@ -538,6 +556,7 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
     g.nbp = (uint32_t)nbp;
     g.bytes = (uint32_t)bytes;
     g.y = t[i].y; g.bias = t[i].bias;
+    g.kind = w.type == w0.type ? 0u : 1u;
     g.rows = w.rows;
     g.tiles = (w.rows + p.RT - 1) / p.RT;
   }
@@ -549,10 +568,12 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   m.oq = QXOut{};
   m.oq_norm = nullptr;
   if (qout) { m.oq = out->q; m.oq_norm = out->norm_w; }
+  if (other == Q6_K) return launch_t<CQ4K, CQ6K, false>(s, m, p);  // w0 is Q4_K
+  if (other == Q4_K) return launch_t<CQ6K, CQ4K, false>(s, m, p);
   switch (w0.type) {
-    case Q4_K: return glu ? launch_t<CQ4K, true>(s, m, p) : launch_t<CQ4K, false>(s, m, p);
-    case Q6_K: return glu ? launch_t<CQ6K, true>(s, m, p) : launch_t<CQ6K, false>(s, m, p);
-    case Q8_0: return glu ? launch_t<CQ80, true>(s, m, p) : launch_t<CQ80, false>(s, m, p);
+    case Q4_K: return glu ? launch_t<CQ4K, CQ4K, true>(s, m, p) : launch_t<CQ4K, CQ4K, false>(s, m, p);
+    case Q6_K: return glu ? launch_t<CQ6K, CQ6K, true>(s, m, p) : launch_t<CQ6K, CQ6K, false>(s, m, p);
+    case Q8_0: return glu ? launch_t<CQ80, CQ80, true>(s, m, p) : launch_t<CQ80, CQ80, false>(s, m, p);
   }
   return hipErrorInvalidValue;
 }

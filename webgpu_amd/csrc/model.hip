@@ -69,8 +69,8 @@ struct wgd_model {
   // in the QX format.
   bool qpath = false;
   bool fused_attention = false;  // decode attention in one pass (head dims 64 / 128 / 256)
-  // RoPE (cos, sin) tables of the decode attention: [0] the model's theta, [1] Gemma's local
-  float2 *rope_tab[2] = {nullptr, nullptr};
+  // RoPE inverse frequencies of the decode attention: [0] the model's theta, [1] Gemma's local
+  double *inv_freq[2] = {nullptr, nullptr};
   void *qx_attn = nullptr, *qx_ffn = nullptr, *qx_o = nullptr, *qx_down = nullptr, *qx_head = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -141,12 +141,12 @@ hipError_t decode_attention_layer(wgd_model *m, int l, const QXOut &qx) {
   a.partial = m->att_part; a.y = m->att; a.qx = qx; a.pos = &m->state->pos;
   a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = c.head_dim; a.capacity = L.cap; a.window = window_of(m, l);
   a.scale = c.attention_scale; a.eps = c.epsilon;
-  a.rope_table = m->rope_tab[0]; a.rope_positions = (uint32_t)c.context;
+  a.inv_freq = m->inv_freq[0];
   if (is_gemma(m)) {
     a.mode = 0; a.rot = 0; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
     a.theta = local_layer(m, l) ? c.local_theta : c.theta;
     a.rope_scale = local_layer(m, l) ? 1.f : c.rope_scale;
-    if (local_layer(m, l)) a.rope_table = m->rope_tab[1];
+    if (local_layer(m, l)) a.inv_freq = m->inv_freq[1];
   } else if (c.qk_norm) {
     a.mode = 0; a.rot = c.rotary_dim; a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.theta = c.theta; a.rope_scale = c.rope_scale;
   } else {
@@ -216,15 +216,18 @@ __global__ void k_advance(StepState *st, const int32_t *arg, int32_t *tokens, ui
 
 QXView qv(void *p, uint32_t K, bool normed = false, float eps = 0.f) { return qx_const(qx_view(p, K), K, normed, eps); }
 
-// Matvecs of several matrices that read the same activation, one launch per weight type.
+// Matvecs of several matrices that read the same activation: one launch for K-quants
+// (Q4_K and Q6_K mix), else one per weight type.
 hipError_t mv_group(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x) {
+  auto kq = [](int type) { return type == Q4_K || type == Q6_K; };
+  auto same = [&](int a, int b) { return a == b || (kq(a) && kq(b)); };
   bool done[MV_MAX_SEGS] = {};
   for (uint32_t i = 0; i < n; i++) {
     if (done[i]) continue;
     MVTarget grp[MV_MAX_SEGS];
     uint32_t k = 0;
     for (uint32_t j = i; j < n; j++)
-      if (!done[j] && t[j].w->type == t[i].w->type) { grp[k++] = t[j]; done[j] = true; }
+      if (!done[j] && same(t[j].w->type, t[i].w->type)) { grp[k++] = t[j]; done[j] = true; }
     WGD_HIP(mv(s, grp, k, x, MV_STORE));
   }
   return hipSuccess;
@@ -565,14 +568,13 @@ int wgd_model_ready(wgd_model *m) {
     const char *fa = getenv("WGD_FUSED_ATTENTION");
     m->fused_attention = decode_attention_supported(c.heads, c.kv_heads, c.head_dim) && norms && !(fa && fa[0] == '0');
     if (m->fused_attention) {
-      // one table per distinct (theta, scale): the model's, and Gemma's local layers'
+      // one table per distinct theta: the model's, and Gemma's local layers'
       const uint32_t rot = is_gemma(m) || !c.rotary_dim ? (uint32_t)c.head_dim : (uint32_t)c.rotary_dim;
-      const uint64_t n = (uint64_t)c.context * (rot / 2);
-      rc = alloc_t(m, n * 2, "rope table", (float **)&m->rope_tab[0]);
-      if (!rc) rc = ctx_check(ctx, rope_table(ctx->stream, m->rope_tab[0], (uint32_t)c.context, rot, c.theta, c.rope_scale), "rope table");
+      rc = alloc_t(m, rot / 2, "rope frequencies", &m->inv_freq[0]);
+      if (!rc) rc = ctx_check(ctx, rope_inv_freq(ctx->stream, m->inv_freq[0], rot, c.theta), "rope frequencies");
       if (!rc && is_gemma(m)) {
-        rc = alloc_t(m, n * 2, "rope table (local)", (float **)&m->rope_tab[1]);
-        if (!rc) rc = ctx_check(ctx, rope_table(ctx->stream, m->rope_tab[1], (uint32_t)c.context, rot, c.local_theta, 1.f), "rope table");
+        rc = alloc_t(m, rot / 2, "rope frequencies (local)", &m->inv_freq[1]);
+        if (!rc) rc = ctx_check(ctx, rope_inv_freq(ctx->stream, m->inv_freq[1], rot, c.local_theta), "rope frequencies");
       }
       if (rc) return rc;
     }
