@@ -11,8 +11,9 @@ roofline: the Q4_K dequant-matvec at the 14336x4096 FFN shape (ne0 = 14336 input
 4096 outputs), timed with a HIP event pair around every launch on the library's stream,
 rotating 24 distinct weight copies (~800 MB, far beyond the 256 MB Infinity Cache) so the
 bytes come from HBM. achieved = algorithmic bytes (weights + 4*in + 4*out) / mean launch
-time. The other microbench shapes (4096x4096, 4096x14336 Q4_K; 4096x128256 Q6_K) are
-reported under "matvec".
+time. traffic = HBM bytes per launch from the committed rocprofv3 counter summary of the
+same microbench (profiles/k_mv_matvec_microbench.md). The other microbench shapes (4096x4096,
+4096x14336 Q4_K; 4096x128256 Q6_K) are reported under "matvec".
 
 cpu_baseline: the float64 C oracle (OpenMP over the host cores) decoding the same 8B
 model on a bounded sample (8-token prompt, then as many greedy tokens as fit ~15 s).
@@ -38,6 +39,22 @@ from webgpu_amd.gguf import Q4_K, Q6_K, QUANTS  # noqa: E402
 from webgpu_amd.gpu import Compute  # noqa: E402
 
 PEAK_HBM = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
+# HBM bytes per launch of the roofline kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE scaled by a
+# 256 MiB copy in the same program (the summary holds the commands and the raw counts).
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mv_matvec_microbench.md")
+
+
+def profiled_traffic(type_name: str, shape: str):
+    """traffic_bytes line of the committed counter summary for this shape, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                f = line.split()
+                if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == type_name and f[2] == shape:
+                    return int(f[3])
+    except OSError:
+        pass
+    return None
 METRIC = "decode tok/s (1 GPU) + Q4_K matvec HBM GB/s as % of peak"
 
 
@@ -144,11 +161,30 @@ def main() -> None:
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-matvec", action="store_true", help="skip the matvec microbench")
+    ap.add_argument("--matvec-only", action="store_true",
+                    help="only the matvec microbench and a 256 MiB device copy (counter calibration), no JSON line")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the token loop runs on a single MI355X (multi-GPU sharding is a design "
               "only); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if a.matvec_only:
+        gpu = Compute().init()
+        ev = Events()
+        # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch scale the counters
+        n = 256 << 20
+        src, dst = gpu.buffer(n, "copy src"), gpu.buffer(n, "copy dst")
+        for _ in range(4):
+            gpu.copy(src, dst, n)
+        gpu.done()
+        gpu.destroy(src)
+        gpu.destroy(dst)
+        for s in [(Q4_K, 14336, 4096), (Q4_K, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 4096, 128256)]:
+            m = matvec_bench(gpu, ev, *s)
+            print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
+                  f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+        gpu.dispose()
+        return
     context = 1024
     if a.prompt + a.warmup + a.steps > context:
         context = min(32768, 1 << (a.prompt + a.warmup + a.steps - 1).bit_length())
@@ -206,7 +242,7 @@ def main() -> None:
         gpu.dispose()
         head = mv[0]
         result["roofline"] = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                              "frac": head["frac"], "traffic": None,
+                              "frac": head["frac"], "traffic": profiled_traffic(head["type"], head["shape"]),
                               "kernel": f"k_matvec<Q4K> {head['shape']} (in x out), {head['bytes']} B per launch",
                               "mean_us": head["us"]}
         result["matvec"] = mv

@@ -70,10 +70,11 @@ int wgd_buffer_create(wgd_context *ctx, uint64_t size, const char *label, wgd_bu
 int wgd_buffer_destroy(wgd_context *ctx, wgd_buffer *buf);
 uint64_t wgd_buffer_size(const wgd_buffer *buf);
 /* WeightPager.page (pager.ts:25-44) with paging collapsed: upload a whole rows x cols weight
- * matrix of GGUF `type` once, in the layout the kernels read fastest. Q6_K and Q8_0 blocks
- * (210 and 34 bytes, so not 16-byte aligned) are split into aligned planes of the same bytes;
- * other types keep the GGUF bytes. Decoded values are unchanged. The buffer is accepted by
- * wgd_matmul and wgd_embed for that type and shape. `bytes` must equal rows*rowBytes. */
+ * matrix of GGUF `type` once, in the layout the kernels read fastest. Q4_K, Q6_K and Q8_0
+ * are rearranged on the device into a planar layout of the same bits (16-byte quant chunks
+ * tiled by 16 rows, block headers/scales in separate planes); other types keep the GGUF
+ * bytes. Decoded values are unchanged. The buffer is accepted by wgd_matmul, wgd_matvec and
+ * wgd_embed for that type and shape. `bytes` must equal rows*rowBytes. */
 int wgd_upload_weights(wgd_context *ctx, int32_t type, uint32_t cols, uint32_t rows,
                        const void *data, uint64_t bytes, const char *label, wgd_buffer **out);
 /* The context's HIP stream (hipStream_t), for hosts that time or order work against it. */

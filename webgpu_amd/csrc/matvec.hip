@@ -20,8 +20,9 @@
 // Memory: planar row-tiled weights (quant.hip): one load instruction of a wavefront reads 16
 // rows x 4 chunks = 1 KB contiguous; raw buffer loads with the per-unit offset in an SGPR.
 // Each wavefront keeps DU units of loads in flight (software pipeline over registers). The
-// activation digits are staged once per workgroup in LDS, after the first weight loads are
-// issued. Per row step each lane leaves its partial sum in LDS; the first RT threads add the
+// activation digits are staged once per workgroup in LDS: their loads are issued before the
+// first weight loads (loads complete in order, so a later issue would wait on every weight
+// load in flight) and written to LDS once they arrive. Per row step each lane leaves its partial sum in LDS; the first RT threads add the
 // K slices and column groups in a fixed order (deterministic) and run the epilogue: store,
 // residual add, or the gated SwiGLU/GeGLU of a gate/up pair, optionally re-quantizing the
 // result (times the next RMSNorm weight) for the next matvec. Nothing synchronizes across
