@@ -29,11 +29,29 @@ QXOut qx_view(void *base, uint32_t K);
 QXView qx_const(const QXOut &q, uint32_t K, bool normed, float eps);
 
 #ifdef __HIPCC__
+// Max / sum over each aligned 16-lane row of the wavefront, left in every lane of the row:
+// DPP quad xor 1, quad xor 2, half-row mirror, row mirror (VALU moves, no LDS round trip).
+// Every lane of the row must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  return fmaxf(v, dpp_mov<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  return v + dpp_mov<0x140>(v);
+}
+
 // Quantizes one value per lane in aligned 16-lane groups; the block scale is max|v| / 127.
 __device__ __forceinline__ void quant_lane16(float v, float &scale, int &d0, int &d1, int &d2) {
-  float a = fabsf(v);
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  const float a = row16_max(fabsf(v));
   scale = a * (1.f / 127.f);
   const float u = a > 0.f ? v * (127.f / a) : 0.f;
   const float r0 = fminf(fmaxf(rintf(u), -127.f), 127.f);
@@ -49,9 +67,7 @@ __device__ __forceinline__ void quant_lane16(float v, float &scale, int &d0, int
 __device__ __forceinline__ void qx_store(const QXOut &q, uint32_t i, float v, float raw, bool live) {
   float sc; int d0, d1, d2;
   quant_lane16(live ? v : 0.f, sc, d0, d1, d2);
-  float s16 = live ? v : 0.f, q16 = live ? raw * raw : 0.f;
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) { s16 += __shfl_xor(s16, o, 64); q16 += __shfl_xor(q16, o, 64); }
+  const float s16 = row16_sum(live ? v : 0.f), q16 = row16_sum(live ? raw * raw : 0.f);
   if (live) {
     q.d0[i] = (int8_t)d0; q.d1[i] = (int8_t)d1; q.d2[i] = (int8_t)d2;
     if ((i & 15) == 0) { q.scale[i >> 4] = sc; q.sum[i >> 4] = s16; q.sq[i >> 4] = q16; }

@@ -76,6 +76,12 @@ __device__ __forceinline__ uint2 bl8(Rsrc r, uint32_t v, uint32_t s) {
 __device__ __forceinline__ uint32_t bl2(Rsrc r, uint32_t v, uint32_t s) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, v, s, CPOL_NT);
 }
+// Activation loads: cached (every workgroup reads the same vector), zero past the plane.
+__device__ __forceinline__ uint4 bl16c(Rsrc r, uint32_t v) {
+  const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, v, 0, 0);
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+__device__ __forceinline__ uint32_t bl4c(Rsrc r, uint32_t v) { return __builtin_amdgcn_raw_buffer_load_b32(r, v, 0, 0); }
 __device__ __forceinline__ float f16lo(uint32_t v) { return __half2float(__ushort_as_half((unsigned short)(v & 0xFFFFu))); }
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b) {
@@ -115,14 +121,12 @@ struct CQ4K {
     // digit sums of 16 4-bit weights fit int32 weighted by 254^2, 254, 1 (|d0 sum| <= 16 * 15 * 127)
     const int tl = __mul24(dl[0], 64516) + __mul24(dl[1], 254) + dl[2];
     const int th = __mul24(dh[0], 64516) + __mul24(dh[1], 254) + dh[2];
-    uint32_t sc, mn;
-    if ((cb & 4) == 0) {  // uniform
-      sc = __builtin_amdgcn_ubfe(r.h.y, l.s6, 6);
-      mn = __builtin_amdgcn_ubfe(r.h.z, l.s6, 6);
-    } else {
-      sc = __builtin_amdgcn_ubfe(r.h.w, l.s4, 4) | (__builtin_amdgcn_ubfe(r.h.y, l.sh, 2) << 4);
-      mn = __builtin_amdgcn_ubfe(r.h.w, l.sm, 4) | (__builtin_amdgcn_ubfe(r.h.z, l.sh, 2) << 4);
-    }
+    // both packings, selected by the (uniform) quad parity: no branch in the unit's code
+    const uint32_t sce = __builtin_amdgcn_ubfe(r.h.y, l.s6, 6), mne = __builtin_amdgcn_ubfe(r.h.z, l.s6, 6);
+    const uint32_t sco = __builtin_amdgcn_ubfe(r.h.w, l.s4, 4) | (__builtin_amdgcn_ubfe(r.h.y, l.sh, 2) << 4);
+    const uint32_t mno = __builtin_amdgcn_ubfe(r.h.w, l.sm, 4) | (__builtin_amdgcn_ubfe(r.h.z, l.sh, 2) << 4);
+    const bool odd = (cb & 4) != 0;
+    const uint32_t sc = odd ? sco : sce, mn = odd ? mno : mne;
     const float S_ = x.s[0] * (float)tl + x.s[1] * (float)th;
     return f16lo(r.h.x) * (float)sc * S_ - f16lo(r.h.x >> 16) * (float)mn * (x.m[0] + x.m[1]);
   }
@@ -190,22 +194,38 @@ __device__ __forceinline__ float gelu_tanh_mv(float g) {
   return 0.5f * g * (1.f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g)));
 }
 
+// Per-row inputs of the epilogue (residual, bias, next norm weight), loaded at the start of
+// the workgroup so their latency hides behind the weight stream: raw buffer loads that read
+// zero past the segment's rows, or for an absent input.
+struct RowIn { float y, bias, norm; };
+__device__ __forceinline__ RowIn row_inputs(const MV &m, const MVSeg &g, uint32_t row) {
+  const uint32_t nb = 4 * g.rows;
+  const Rsrc ry = make_rsrc((const uint8_t *)g.y, m.epi == MV_ADD ? nb : 0);
+  const Rsrc rb = make_rsrc((const uint8_t *)g.bias, g.bias ? nb : 0);
+  const Rsrc rn = make_rsrc((const uint8_t *)m.oq_norm, (m.oq.d0 && m.oq_norm) ? nb : 0);
+  RowIn in;
+  in.y = __uint_as_float(bl4c(ry, 4 * row));
+  in.bias = __uint_as_float(bl4c(rb, 4 * row));
+  in.norm = __uint_as_float(bl4c(rn, 4 * row));
+  return in;
+}
+
 // Epilogue of one row: thread t < RT holds row row0 + t of segment g.
-__device__ __forceinline__ void finish_row(const MV &m, const MVSeg &g, uint32_t row, bool live, float v, float u) {
+__device__ __forceinline__ void finish_row(const MV &m, const MVSeg &g, uint32_t row, bool live, float v, float u,
+                                           const RowIn &in) {
   float out = 0.f;
   if (live) {
-    if (g.bias) v += g.bias[row];
-    float *dst = g.y + row;
+    v += in.bias;
     switch (m.epi) {
       case MV_STORE: out = v; break;
-      case MV_ADD: out = *dst + v; break;
+      case MV_ADD: out = in.y + v; break;
       case MV_SILU: out = v / (1.f + expf(-v)) * u; break;
       case MV_GELU: out = gelu_tanh_mv(v) * u; break;
     }
-    *dst = out;
+    g.y[row] = out;
   }
   if (m.oq.d0) {
-    const float wn = (live && m.oq_norm) ? m.oq_norm[row] : 1.f;
+    const float wn = (live && m.oq_norm) ? in.norm : 1.f;
     qx_store(m.oq, row, out * wn, out, live);
   }
 }
@@ -239,8 +259,11 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   const uint32_t r = lane & 15, gq = lane >> 4;
   const typename T::L lc = T::lane(r, gq);
   // unit u of this wavefront: step u / NSB (tile tile0 + rg + step * NR), quad (s * NSB + u % NSB)
+  // (uniform: readfirstlane keeps the load offsets in SGPRs whatever the divergence analysis
+  // concludes about the loop counters)
   auto unit_of = [&](uint32_t step, uint32_t sl) -> Unit {
-    return Unit{tile0 + rg + step * m.NR, 4 * (s * m.NSB + sl)};
+    return Unit{(uint32_t)__builtin_amdgcn_readfirstlane(tile0 + rg + step * m.NR),
+                (uint32_t)__builtin_amdgcn_readfirstlane(4 * (s * m.NSB + sl))};
   };
   typename T::W buf[DU], buf1[GLU ? DU : 1];
   uint32_t is_step = 0, is_sl = 0;  // next unit to issue
@@ -252,30 +275,38 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   };
   // The activation is staged in LDS; its loads (from L2) go out first and the first DU units
   // of weight loads right after, so the wait for the activation does not include the weights
-  // (loads complete in issue order for the wait counter). Up to XJ 16-byte pieces per plane
-  // and XB blocks per thread are held in registers; any rest is staged afterwards.
+  // (loads complete in issue order for the wait counter). The activation loads are raw buffer
+  // loads that read zero past each plane, so they need no branches, and nothing uses their
+  // values before the weight loads are issued: any arithmetic on them there would make the
+  // compiler wait for them first. Up to XJ 16-byte pieces per plane and XB blocks per thread
+  // are held in registers; any rest is staged afterwards.
   constexpr uint32_t XJ = 2, XB = 2;
   const uint32_t nt = blockDim.x, tid = threadIdx.x;
   const uint32_t kq = (m.x.len + 63) / 64 * 64;  // QX planes hold Kp elements
-  const uint32_t pieces = m.ke / 16, blocks = m.ke / 16, live = m.x.len / 16;
+  const uint32_t blocks = m.ke / 16, live = m.x.len / 16;
+  const Rsrc rxd[3] = {make_rsrc((const uint8_t *)m.x.d[0], kq), make_rsrc((const uint8_t *)m.x.d[1], kq),
+                       make_rsrc((const uint8_t *)m.x.d[2], kq)};
+  const Rsrc rxs = make_rsrc((const uint8_t *)m.x.scale, 4 * live), rxm = make_rsrc((const uint8_t *)m.x.sum, 4 * live);
+  const Rsrc rxq = make_rsrc((const uint8_t *)m.x.sq, m.x.normed ? 4 * live : 0);
+  const RowIn rin = row_inputs(m, g, row0 + tid);  // used by threads tid < RT
   uint4 xd[3][XJ];
-  float xsc[XB], xsm[XB], ss = 0.f;
+  uint32_t xsc[XB], xsm[XB], xsq[XB];
 #pragma unroll
   for (uint32_t j = 0; j < XJ; j++) {
     const uint32_t e = (tid + j * nt) * 16;
 #pragma unroll
-    for (int p = 0; p < 3; p++) xd[p][j] = e < kq ? *(const uint4 *)(m.x.d[p] + e) : make_uint4(0, 0, 0, 0);
+    for (int p = 0; p < 3; p++) xd[p][j] = bl16c(rxd[p], e);
   }
 #pragma unroll
   for (uint32_t j = 0; j < XB; j++) {
-    const uint32_t i = tid + j * nt;
-    const bool in = i < live;
-    xsc[j] = in ? m.x.scale[i] : 0.f;
-    xsm[j] = in ? m.x.sum[i] : 0.f;
-    if (m.x.normed && in) ss += m.x.sq[i];
+    const uint32_t i = 4 * (tid + j * nt);
+    xsc[j] = bl4c(rxs, i);
+    xsm[j] = bl4c(rxm, i);
+    xsq[j] = bl4c(rxq, i);
   }
 #pragma unroll
   for (int d = 0; d < DU; d++) issue(d);
+  __builtin_amdgcn_sched_barrier(0);
   if (tid < 2) *(uint4 *)(lds + 16 * tid) = make_uint4(0, 0, 0, 0);
 #pragma unroll
   for (uint32_t j = 0; j < XJ; j++) {
@@ -284,22 +315,23 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
 #pragma unroll
       for (int p = 0; p < 3; p++) *(uint4 *)(lds + L.digits + p * m.ke + e) = xd[p][j];
   }
+  float ss = 0.f;
 #pragma unroll
   for (uint32_t j = 0; j < XB; j++) {
     const uint32_t i = tid + j * nt;
     if (i < blocks) {
-      ((float *)(lds + L.scale))[i] = xsc[j] * (1.f / 64516.f);
-      ((float *)(lds + L.sum))[i] = xsm[j];
+      ((float *)(lds + L.scale))[i] = __uint_as_float(xsc[j]) * (1.f / 64516.f);
+      ((float *)(lds + L.sum))[i] = __uint_as_float(xsm[j]);
     }
+    ss += __uint_as_float(xsq[j]);
   }
   for (uint32_t e = (tid + XJ * nt) * 16; e < m.ke; e += nt * 16)
-    for (int p = 0; p < 3; p++)
-      *(uint4 *)(lds + L.digits + p * m.ke + e) = e < kq ? *(const uint4 *)(m.x.d[p] + e) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int p = 0; p < 3; p++) *(uint4 *)(lds + L.digits + p * m.ke + e) = bl16c(rxd[p], e);
   for (uint32_t i = tid + XB * nt; i < blocks; i += nt) {
-    const bool in = i < live;
-    ((float *)(lds + L.scale))[i] = in ? m.x.scale[i] * (1.f / 64516.f) : 0.f;
-    ((float *)(lds + L.sum))[i] = in ? m.x.sum[i] : 0.f;
-    if (m.x.normed && in) ss += m.x.sq[i];
+    ((float *)(lds + L.scale))[i] = __uint_as_float(bl4c(rxs, 4 * i)) * (1.f / 64516.f);
+    ((float *)(lds + L.sum))[i] = __uint_as_float(bl4c(rxm, 4 * i));
+    ss += __uint_as_float(bl4c(rxq, 4 * i));
   }
   if (m.x.normed) {
     ss = wave_sum(ss);
@@ -311,10 +343,13 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   const bool diag = (r >> 2) == gq && (r & 3) < 3;
   const uint32_t amask = diag ? 0xFFFFFFFFu : 0u;
   const uint32_t abase = L.digits + (r & 3) * m.ke + T::N * gq;
-  uint32_t cs_step = 0, cs_sl = 0;  // next unit to compute
+  // Units are computed in chunks of DU (DU divides NSB, so a chunk never straddles a row
+  // step); the per-unit code has no branches, so the compiler can overlap the LDS reads and
+  // MFMAs of a chunk's units. A step's partial sums go to LDS after its last chunk.
+  uint32_t cs_step = 0, cs_sl = 0;  // first unit of the next chunk
   float acc = 0.f, acc1 = 0.f;
-  auto compute = [&](int slot) {
-    const Unit u = unit_of(cs_step, cs_sl);
+  auto compute = [&](int slot, uint32_t sl) {
+    const Unit u = unit_of(cs_step, sl);
     XA xa;
     const uint32_t ad = (abase + T::N * u.cb) & amask;
     xa.a[0] = *(const v4i *)(lds + ad);
@@ -329,7 +364,10 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
     }
     acc += T::dot(buf[slot], lc, xa, u.cb);
     if (GLU) acc1 += T::dot(buf1[slot], lc, xa, u.cb);
-    if (++cs_sl == m.NSB) {
+  };
+  auto chunk_done = [&]() {
+    cs_sl += DU;
+    if (cs_sl == m.NSB) {
       // step done: this lane's partial of row (rg + step * NR) * 16 + r, K slice s, group gq
       const uint32_t rr = (rg + cs_step * m.NR) * 16 + r;
       ((float *)(lds + L.vals))[(s * m.RT + rr) * 4 + gq] = acc;
@@ -339,16 +377,17 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
     }
   };
   // sliding window: U is a multiple of DU
-  uint32_t u0 = 0;
-  for (; u0 + DU < m.U; u0 += DU) {
+  for (uint32_t u0 = DU; u0 < m.U; u0 += DU) {
 #pragma unroll
     for (int d = 0; d < DU; d++) {
-      compute(d);
+      compute(d, cs_sl + d);
       issue(d);
     }
+    chunk_done();
   }
 #pragma unroll
-  for (int d = 0; d < DU; d++) compute(d);
+  for (int d = 0; d < DU; d++) compute(d, cs_sl + d);
+  chunk_done();
   __syncthreads();
   if (threadIdx.x >= ((m.RT + 63) & ~63u)) return;
   float xm = 1.f;
@@ -371,7 +410,7 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
       }
     }
   }
-  finish_row(m, g, row0 + row, inside, v * xm, v1 * xm);
+  finish_row(m, g, row0 + row, inside, v * xm, v1 * xm, rin);
 }
 
 // One workgroup per row tile. T1 is the chunk type of segments with kind 1 (Q and K in
@@ -465,9 +504,9 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
         const LdsMap lm = lds_map(ke, ns, rt, glu);
         if (lm.bytes > lds_limit()) break;
         const uint32_t units = iter * nsb;
-        uint32_t du = dumax;
-        while (du > 1 && units % du) du /= 2;
-        if (env_du) { if (units % (uint32_t)env_du || (uint32_t)env_du > dumax) continue; du = (uint32_t)env_du; }
+        uint32_t du = dumax;  // a chunk of DU units stays within one row step
+        while (du > 1 && nsb % du) du /= 2;
+        if (env_du) { if (nsb % (uint32_t)env_du || (uint32_t)env_du > dumax) continue; du = (uint32_t)env_du; }
         uint32_t tiles = 0;
         for (uint32_t i = 0; i < n; i++) tiles += (rows[i] + rt - 1) / rt;
         const uint32_t rounds = (tiles + cus - 1) / cus;
@@ -542,7 +581,7 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
     rows[i] = w.rows;
   }
   const MVPlan p = mv_plan(w0, rows, n, glu, qout);
-  if (!p.RT || p.threads != 64 * p.NS * p.NR || p.threads > 1024 || p.RT > p.threads || (p.ITER * p.NSB) % p.DU ||
+  if (!p.RT || p.threads != 64 * p.NS * p.NR || p.threads > 1024 || p.RT > p.threads || p.NSB % p.DU ||
       p.lds > lds_limit() || (qout && p.RT % 16))
     return hipErrorInvalidValue;
   MV m{};
