@@ -245,11 +245,35 @@ constexpr uint32_t AD_WAVES = 4;
 struct AttnDecK {
   const float *q, *k, *v; float *kc, *vc; const float *qn, *kn; float *part;
   const int32_t *pos;
-  const double *invf;
-
+  const float *cs;   // this token's rotation: cos of pair i at [i], sin at [rot / 2 + i]
   uint32_t heads, kvh, rot, cap, window, group, chunk, nsplit;
-  float scale, theta, rscale, eps; int mode;
+  float scale, eps; int mode;
 };
+
+// Chunk epilogue of both decode kernels: merge the four wavefronts' (max, sum, output) into
+// the chunk's partial, which k_attn_comb merges with the other chunks of the head.
+template <int G, uint32_t HD>
+__device__ __forceinline__ void chunk_epilogue(const AttnDecK &a, uint32_t kv, uint32_t z, const float (*wm)[G],
+                                               const float (*wl)[G], const float (*wo)[G][HD]) {
+  const uint32_t g = a.group;
+  for (uint32_t j = threadIdx.x; j < g * HD; j += blockDim.x) {
+    const uint32_t i = j / HD, d = j % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) M = fmaxf(M, wm[u][i]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) {
+      if (wm[u][i] == -INFINITY) continue;
+      const float f = expf(wm[u][i] - M);
+      L += wl[u][i] * f;
+      O += wo[u][i][d] * f;
+    }
+    float *pp = a.part + (((uint64_t)kv * g + i) * a.nsplit + z) * (HD + 2);
+    if (d == 0) { pp[0] = M; pp[1] = L; }
+    pp[2 + d] = O;
+  }
+}
 
 template <int EL, int G>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
@@ -283,11 +307,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
   // ---- prologue: Q/K norm and RoPE of the group's query heads and the new key
   const uint32_t half = a.rot / 2;
   for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
-    const double angle = (double)pos * (double)a.rscale * a.invf[i];
-    double sd, cd;
-    sincos(angle, &sd, &cd);
-    csn[2 * i] = (float)cd;
-    csn[2 * i + 1] = (float)sd;
+    csn[2 * i] = a.cs[i];
+    csn[2 * i + 1] = a.cs[half + i];
   }
   for (uint32_t it = w; it <= g; it += AD_WAVES) {
     const bool isk = it == g;
@@ -379,7 +400,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
       m[i] = mn;
     }
   }
-  // ---- merge the wavefronts
+  // ---- merge the wavefronts, then the chunks
 #pragma unroll
   for (int i = 0; i < G; i++) {
     if (lane == 0) { wm[w][i] = m[i]; wl[w][i] = l[i]; }
@@ -387,23 +408,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
     for (int e = 0; e < EL; e++) wo[w][i][lane * EL + e] = o[i][e];
   }
   __syncthreads();
-  for (uint32_t j = threadIdx.x; j < g * HD; j += blockDim.x) {
-    const uint32_t i = j / HD, d = j % HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (uint32_t u = 0; u < AD_WAVES; u++) M = fmaxf(M, wm[u][i]);
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (uint32_t u = 0; u < AD_WAVES; u++) {
-      if (wm[u][i] == -INFINITY) continue;
-      const float f = expf(wm[u][i] - M);
-      L += wl[u][i] * f;
-      O += wo[u][i][d] * f;
-    }
-    float *pp = a.part + (((uint64_t)kv * g + i) * a.nsplit + z) * (HD + 2);
-    if (d == 0) { pp[0] = M; pp[1] = L; }
-    pp[2 + d] = O;
-  }
+  chunk_epilogue<G, HD>(a, kv, z, wm, wl, wo);
 }
 
 // The same step with everything a lane needs kept in registers: lane l holds elements
@@ -432,9 +437,13 @@ __global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
     qw[e] = a.mode == 0 ? a.qn[el(e)] : 1.f;
     kw[e] = a.mode == 0 ? a.kn[el(e)] : 1.f;
   }
-  double f[NP];
+  float cr[NP], sr[NP];
 #pragma unroll
-  for (int e = 0; e < (int)NP; e++) f[e] = a.invf[ADJ ? NP * lane + e : lane + 64 * e];
+  for (int e = 0; e < (int)NP; e++) {
+    const uint32_t pi = ADJ ? NP * lane + e : lane + 64 * e;
+    cr[e] = a.cs[pi];
+    sr[e] = a.cs[a.rot / 2 + pi];
+  }
   const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane(*a.pos);
   const uint32_t end = pos + 1, win = end < a.window ? end : a.window, begin = end - win;
   const uint32_t lo = begin + z * a.chunk;
@@ -474,9 +483,7 @@ __global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
   }
 #pragma unroll
   for (int e = 0; e < (int)NP; e++) {
-    double sd, cd;
-    sincos((double)pos * (double)a.rscale * f[e], &sd, &cd);
-    const float c = (float)cd, sn = (float)sd;
+    const float c = cr[e], sn = sr[e];
     const int ia = ADJ ? 2 * e : e, ib = ADJ ? 2 * e + 1 : e + (int)NP;
 #pragma unroll
     for (int i = 0; i < G; i++) {
@@ -541,7 +548,7 @@ __global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
       m[i] = mn;
     }
   }
-  // ---- merge the wavefronts
+  // ---- merge the wavefronts, then the chunks
 #pragma unroll
   for (int i = 0; i < G; i++) {
     if (lane == 0) { wm[w][i] = m[i]; wl[w][i] = l[i]; }
@@ -549,23 +556,7 @@ __global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
     for (int e = 0; e < EL; e++) wo[w][i][el(e)] = o[i][e];
   }
   __syncthreads();
-  for (uint32_t j = threadIdx.x; j < g * HD; j += blockDim.x) {
-    const uint32_t i = j / HD, d = j % HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (uint32_t u = 0; u < AD_WAVES; u++) M = fmaxf(M, wm[u][i]);
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (uint32_t u = 0; u < AD_WAVES; u++) {
-      if (wm[u][i] == -INFINITY) continue;
-      const float fz = expf(wm[u][i] - M);
-      L += wl[u][i] * fz;
-      O += wo[u][i][d] * fz;
-    }
-    float *pp = a.part + (((uint64_t)kv * g + i) * a.nsplit + z) * (HD + 2);
-    if (d == 0) { pp[0] = M; pp[1] = L; }
-    pp[2 + d] = O;
-  }
+  chunk_epilogue<G, HD>(a, kv, z, wm, wl, wo);
 }
 
 // Merge of the chunks of one query head: thread d owns output element d. The partials were
@@ -647,8 +638,8 @@ uint64_t decode_attention_scratch_floats(uint32_t heads, uint32_t kv_heads, uint
 
 template <int EL>
 static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
-  // registers only: full-width rotation with its pairs inside a lane (EL >= 2)
-  const bool fast = EL >= 2 && (k.mode == 2 || k.rot == 64u * EL);
+  // registers only: full-width rotation (rot == hd) with its pairs inside a lane (EL >= 2)
+  const bool fast = EL >= 2 && k.rot == 64u * EL;
   if (fast) {
     constexpr int E = EL >= 2 ? EL : 2;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, k); };
@@ -669,18 +660,18 @@ static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
 
 hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
   if (!decode_attention_supported(in.heads, in.kv_heads, in.hd) || !in.capacity || !in.window || !in.pos ||
-      !in.partial || !in.inv_freq || (in.mode == 0 && (!in.q_norm || !in.k_norm)) || in.rot > in.hd || in.rot % 2)
+      !in.partial || !in.rope || !in.y || (in.mode == 0 && (!in.q_norm || !in.k_norm)) || in.rot > in.hd || in.rot % 2)
     return hipErrorInvalidValue;
   AttnDecK k;
   k.q = in.q; k.k = in.k; k.v = in.v; k.kc = in.kc; k.vc = in.vc; k.qn = in.q_norm; k.kn = in.k_norm;
-  k.part = in.partial; k.pos = in.pos; k.invf = in.inv_freq;
+  k.part = in.partial; k.pos = in.pos; k.cs = in.rope;
   k.heads = in.heads; k.kvh = in.kv_heads; k.rot = in.rot ? in.rot : in.hd; k.cap = in.capacity;
   k.window = in.window; k.group = in.heads / in.kv_heads;
   k.chunk = dec_chunk(in.capacity, in.kv_heads);
   const uint32_t keys = in.window < in.capacity ? in.window : in.capacity;
   k.nsplit = (keys + k.chunk - 1) / k.chunk;
   if (k.nsplit > AD_MAX_SPLITS) return hipErrorInvalidValue;
-  k.scale = in.scale; k.theta = in.theta; k.rscale = in.rope_scale; k.eps = in.eps; k.mode = in.mode;
+  k.scale = in.scale; k.eps = in.eps; k.mode = in.mode;
   const dim3 grid(in.kv_heads, k.nsplit);
   if (in.hd == 64) launch_dec<1>(s, k, grid);
   else if (in.hd == 128) launch_dec<2>(s, k, grid);

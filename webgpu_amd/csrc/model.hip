@@ -71,6 +71,7 @@ struct wgd_model {
   bool fused_attention = false;  // decode attention in one pass (head dims 64 / 128 / 256)
   // RoPE inverse frequencies of the decode attention: [0] the model's theta, [1] Gemma's local
   double *inv_freq[2] = {nullptr, nullptr};
+  float *rope_cs[2] = {nullptr, nullptr};  // this token's rotation tables (token_start)
   void *qx_attn = nullptr, *qx_ffn = nullptr, *qx_o = nullptr, *qx_down = nullptr, *qx_head = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -141,16 +142,14 @@ hipError_t decode_attention_layer(wgd_model *m, int l, const QXOut &qx) {
   a.partial = m->att_part; a.y = m->att; a.qx = qx; a.pos = &m->state->pos;
   a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = c.head_dim; a.capacity = L.cap; a.window = window_of(m, l);
   a.scale = c.attention_scale; a.eps = c.epsilon;
-  a.inv_freq = m->inv_freq[0];
+  a.rope = m->rope_cs[0];
   if (is_gemma(m)) {
     a.mode = 0; a.rot = 0; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
-    a.theta = local_layer(m, l) ? c.local_theta : c.theta;
-    a.rope_scale = local_layer(m, l) ? 1.f : c.rope_scale;
-    if (local_layer(m, l)) a.inv_freq = m->inv_freq[1];
+    if (local_layer(m, l)) a.rope = m->rope_cs[1];
   } else if (c.qk_norm) {
-    a.mode = 0; a.rot = c.rotary_dim; a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.theta = c.theta; a.rope_scale = c.rope_scale;
+    a.mode = 0; a.rot = c.rotary_dim; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
   } else {
-    a.mode = c.rope_adjacent ? 2 : 1; a.rot = c.rotary_dim; a.theta = c.theta; a.rope_scale = c.rope_scale;
+    a.mode = c.rope_adjacent ? 2 : 1; a.rot = c.rotary_dim;
   }
   return decode_attention(m->ctx->stream, a);
 }
@@ -242,8 +241,18 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
   const uint32_t H = c.hidden, qd = c.heads * c.head_dim, F = c.intermediate;
   const int32_t *pos = &m->state->pos;
   const bool gemma = is_gemma(m);
-  WGD_HIP(embed_matrix(s, m->embd, &m->state->token, m->hidden, 1, c.embed_scale));
-  WGD_HIP(quantize(s, m->hidden, H, m->L[0].attn_norm, qx_view(m->qx_attn, H)));
+  RopeTables rt{};
+  if (m->fused_attention) {
+    // the model's theta (and scale), and Gemma's local theta (scale 1)
+    const uint32_t rot = is_gemma(m) || !c.rotary_dim ? (uint32_t)c.head_dim : (uint32_t)c.rotary_dim;
+    rt.half = rot / 2;
+    rt.n = is_gemma(m) ? 2 : 1;
+    for (uint32_t t = 0; t < rt.n; t++) { rt.freq[t] = m->inv_freq[t]; rt.out[t] = m->rope_cs[t]; }
+    rt.scale[0] = c.rope_scale;
+    rt.scale[1] = 1.f;
+  }
+  WGD_HIP(token_start(s, m->embd, &m->state->token, pos, c.embed_scale, m->hidden, m->L[0].attn_norm,
+                      qx_view(m->qx_attn, H), rt));
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
     MVTarget qkv[3];
@@ -572,9 +581,11 @@ int wgd_model_ready(wgd_model *m) {
       const uint32_t rot = is_gemma(m) || !c.rotary_dim ? (uint32_t)c.head_dim : (uint32_t)c.rotary_dim;
       rc = alloc_t(m, rot / 2, "rope frequencies", &m->inv_freq[0]);
       if (!rc) rc = ctx_check(ctx, rope_inv_freq(ctx->stream, m->inv_freq[0], rot, c.theta), "rope frequencies");
+      if (!rc) rc = alloc_t(m, rot, "rope table", &m->rope_cs[0]);
       if (!rc && is_gemma(m)) {
         rc = alloc_t(m, rot / 2, "rope frequencies (local)", &m->inv_freq[1]);
         if (!rc) rc = ctx_check(ctx, rope_inv_freq(ctx->stream, m->inv_freq[1], rot, c.local_theta), "rope frequencies");
+        if (!rc) rc = alloc_t(m, rot, "rope table (local)", &m->rope_cs[1]);
       }
       if (rc) return rc;
     }

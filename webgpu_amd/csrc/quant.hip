@@ -11,6 +11,8 @@
 #include "internal.h"
 #include "decode.h"
 #include "model.h"
+#include "matvec.h"
+#include "attention.h"
 
 namespace wgd {
 
@@ -86,6 +88,47 @@ hipError_t embed_matrix(hipStream_t s, const Matrix &t, const int32_t *ids, floa
   uint32_t bpr = t.cols / block_size(t.type);
   hipLaunchKernelGGL(k_embed_planar, dim3(gx, n), dim3(256), 0, s, t.type, t.data, (uint64_t)bpr * tile_rows(t.rows), bpr,
                      ids, out, t.cols, scale);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ decode token start
+
+// Workgroups 0 .. ceil(hidden / 256) - 1 gather and quantize 256 elements each (every lane of
+// a 16-lane row takes part in the quantization); the last workgroup forms the rotation tables.
+__global__ __launch_bounds__(256) void k_token_start(Matrix embd, uint32_t bpr, uint64_t rb, const int32_t *token, const int32_t *pos,
+                                                     double scale, float *hidden, const float *norm_w, QXOut q,
+                                                     RopeTables rt) {
+  const uint32_t H = embd.cols;
+  if (blockIdx.x == gridDim.x - 1) {
+    const double p = (double)*pos;
+    for (uint32_t t = 0; t < rt.n; t++)
+      for (uint32_t i = threadIdx.x; i < rt.half; i += blockDim.x) {
+        double sd, cd;
+        sincos(p * (double)rt.scale[t] * rt.freq[t][i], &sd, &cd);
+        rt.out[t][i] = (float)cd;
+        rt.out[t][rt.half + i] = (float)sd;
+      }
+    return;
+  }
+  const uint32_t row = (uint32_t)*token, i = blockIdx.x * 256 + threadIdx.x;
+  const bool live = i < H;
+  float v = 0.f;
+  if (live) {
+    v = embd.layout == LAYOUT_PLANAR ? deq_planar(embd.type, embd.data, (uint64_t)bpr * tile_rows(embd.rows), bpr, H, row, i)
+                                     : deq_elem(embd.type, embd.data + (uint64_t)row * rb, i);
+    if (scale != 1.0) v = (float)((double)v * scale);
+    hidden[i] = v;
+  }
+  qx_store(q, i, live && norm_w ? v * norm_w[i] : v, v, live);
+}
+
+hipError_t token_start(hipStream_t s, const Matrix &embd, const int32_t *token, const int32_t *pos, double scale,
+                       float *hidden, const float *norm_w, const QXOut &q, const RopeTables &rt) {
+  if (!embd.cols || embd.cols % 16 || rt.n > 2 || (rt.n && (!pos || !rt.half))) return hipErrorInvalidValue;
+  const uint32_t bpr = embd.cols / block_size(embd.type);
+  hipLaunchKernelGGL(k_token_start, dim3((embd.cols + 255) / 256 + 1), dim3(256), 0, s, embd, bpr,
+                     row_bytes(embd.type, embd.cols), token, pos, scale,
+                     hidden, norm_w, q, rt);
   return hipGetLastError();
 }
 
