@@ -560,24 +560,29 @@ __global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
 }
 
 // Merge of the chunks of one query head: thread d owns output element d. The partials were
-// written by the previous launch (other XCDs' L2): after the position, every load goes out
-// at once (the first AD_ZB chunks' outputs in registers), so the merge is one round trip.
+// written by the previous launch (other XCDs' L2). Every load goes out at once, before the
+// position arrives: raw buffer loads over the head's nsplit partials (zero past them), the
+// first AD_ZB chunks' outputs in registers; chunks at or past the active count are masked
+// afterwards. So the merge is one round trip.
 constexpr uint32_t AD_MAX_SPLITS = 1024, AD_ZB = 32;
 __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, QXOut qx, const int32_t *pos_dev,
                                                    uint32_t window, uint32_t chunk, uint32_t nsplit, uint32_t hd) {
   __shared__ float wz[AD_MAX_SPLITS];
   __shared__ float red[8];
   const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wv = d >> 6, nw = (blockDim.x + 63) >> 6;
+  const uint32_t stride = hd + 2;
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(part + (uint64_t)h * nsplit * stride), 0, (int)(nsplit * stride * 4), 0x00020000);
+  auto ld = [&](uint32_t idx) { return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, 4 * idx, 0, 0)); };
+  float ov[AD_ZB];
+#pragma unroll
+  for (uint32_t k = 0; k < AD_ZB; k++) ov[k] = ld(k * stride + 2 + (d < hd ? d : 0));
+  const float mz0 = ld(d * stride), lz0 = ld(d * stride + 1);
   const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane(*pos_dev);
   const uint32_t end = pos + 1, win = end < window ? end : window;
   const uint32_t nact = (win + chunk - 1) / chunk;
-  const float *pp = part + (uint64_t)h * nsplit * (hd + 2);
-  float ov[AD_ZB];
-#pragma unroll
-  for (uint32_t k = 0; k < AD_ZB; k++) ov[k] = k < nact && d < hd ? pp[(uint64_t)k * (hd + 2) + 2 + d] : 0.f;
-  float mz = -INFINITY, lz = 0.f;
-  if (d < nact) { mz = pp[(uint64_t)d * (hd + 2)]; lz = pp[(uint64_t)d * (hd + 2) + 1]; }
-  for (uint32_t zz = d + blockDim.x; zz < nact; zz += blockDim.x) mz = fmaxf(mz, pp[(uint64_t)zz * (hd + 2)]);
+  float mz = d < nact ? mz0 : -INFINITY;
+  for (uint32_t zz = d + blockDim.x; zz < nact; zz += blockDim.x) mz = fmaxf(mz, ld(zz * stride));
   float M = mz;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
@@ -586,11 +591,11 @@ __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, 
   M = red[0];
   for (uint32_t u = 1; u < nw; u++) M = fmaxf(M, red[u]);
   float L = 0.f;
-  if (d < nact) { const float f = expf(mz - M); wz[d] = f; L = lz * f; }
+  if (d < nact) { const float f = expf(mz0 - M); wz[d] = f; L = lz0 * f; }
   for (uint32_t zz = d + blockDim.x; zz < nact; zz += blockDim.x) {
-    const float f = expf(pp[(uint64_t)zz * (hd + 2)] - M);
+    const float f = expf(ld(zz * stride) - M);
     wz[zz] = f;
-    L += pp[(uint64_t)zz * (hd + 2) + 1] * f;
+    L += ld(zz * stride + 1) * f;
   }
   L = wave_sum(L);
   __syncthreads();
@@ -602,7 +607,7 @@ __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, 
 #pragma unroll
   for (uint32_t k = 0; k < AD_ZB; k++) if (k < nact) O += ov[k] * wz[k];
   if (d < hd)
-    for (uint32_t k = AD_ZB; k < nact; k++) O += pp[(uint64_t)k * (hd + 2) + 2 + d] * wz[k];
+    for (uint32_t k = AD_ZB; k < nact; k++) O += ld(k * stride + 2 + d) * wz[k];
   const float out = O / L;
   if (d < hd) y[(uint64_t)h * hd + d] = out;
   if (qx.d0) qx_store(qx, h * hd + d, out, out, d < hd);

@@ -115,4 +115,24 @@ __device__ __forceinline__ float segment_sum(float v, int width) {
   return v;
 }
 
+// ------------------------------------------------------------------ argmax keys
+// Key = (order-preserving bits of the value) << 32 | (~index): the largest key is the
+// largest finite value with the lowest index. Non-finite entries never produce a key, so
+// key 0 means "no finite logit".
+__device__ __forceinline__ uint64_t arg_key(float f, uint32_t i) {
+  if (!isfinite(f)) return 0;
+  uint32_t u = f == 0.f ? 0u : __float_as_uint(f);
+  uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - i);
+}
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t lo = __shfl_xor((uint32_t)k, o, 64), hi = __shfl_xor((uint32_t)(k >> 32), o, 64);
+    k = key_max(k, ((uint64_t)hi << 32) | lo);
+  }
+  return k;
+}
+
 }  // namespace wgd

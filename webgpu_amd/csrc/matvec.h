@@ -85,6 +85,8 @@ enum MVEpilogue : int { MV_STORE = 0, MV_ADD = 1, MV_SILU = 2, MV_GELU = 3 };
 struct MVOut {
   QXOut q;
   const float *norm_w = nullptr;
+  uint64_t *arg_part = nullptr;  // argmax key (first index of the finite max) per epilogue wavefront:
+                                 // mv_arg_entries() of them
 };
 
 // One matrix of a launch. Several matrices that read the same activation (the Q, K and V
@@ -122,9 +124,12 @@ struct MV {
   int epi;
   QXOut oq;            // re-quantization of the output (single-matrix launches)
   const float *oq_norm;
+  uint64_t *arg_part;  // argmax key per epilogue wavefront (single-matrix launches)
 };
 
 bool mv_supported(const Matrix &w);
+// Number of argmax keys a single-matrix MV_STORE launch of w writes to MVOut::arg_part.
+uint32_t mv_arg_entries(const Matrix &w);
 MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out);
 // y[r] (op)= mul * sum_c W[r][c] x[c] (+ bias[r]) for each target; epilogue `epi`
 // (store, residual add, or act(W x) * (W1 x) for a gated pair). `out` re-quantizes the

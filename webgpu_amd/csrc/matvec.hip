@@ -211,8 +211,8 @@ __device__ __forceinline__ RowIn row_inputs(const MV &m, const MVSeg &g, uint32_
 }
 
 // Epilogue of one row: thread t < RT holds row row0 + t of segment g.
-__device__ __forceinline__ void finish_row(const MV &m, const MVSeg &g, uint32_t row, bool live, float v, float u,
-                                           const RowIn &in) {
+__device__ __forceinline__ float finish_row(const MV &m, const MVSeg &g, uint32_t row, bool live, float v, float u,
+                                            const RowIn &in) {
   float out = 0.f;
   if (live) {
     v += in.bias;
@@ -228,6 +228,7 @@ __device__ __forceinline__ void finish_row(const MV &m, const MVSeg &g, uint32_t
     const float wn = (live && m.oq_norm) ? in.norm : 1.f;
     qx_store(m.oq, row, out * wn, out, live);
   }
+  return out;
 }
 
 // LDS (dynamic): [0, 32) zeros | digit planes p at 32 + p * ke | block scales / 254^2 and sums
@@ -410,7 +411,12 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
       }
     }
   }
-  finish_row(m, g, row0 + row, inside, v * xm, v1 * xm, rin);
+  const float out = finish_row(m, g, row0 + row, inside, v * xm, v1 * xm, rin);
+  if (m.arg_part) {
+    // argmax key of each epilogue wavefront's rows: entry (workgroup, wavefront)
+    const uint64_t k = wave_max_key(inside ? arg_key(out, row0 + row) : 0);
+    if ((threadIdx.x & 63) == 0) m.arg_part[blockIdx.x * ((m.RT + 63) >> 6) + (threadIdx.x >> 6)] = k;
+  }
 }
 
 // One workgroup per row tile. T1 is the chunk type of segments with kind 1 (Q and K in
@@ -471,6 +477,11 @@ bool mv_supported(const Matrix &w) {
 }
 
 static uint32_t lds_limit() { return 160 * 1024; }
+
+uint32_t mv_arg_entries(const Matrix &w) {
+  const MVPlan p = mv_plan(w, &w.rows, 1, false, false);
+  return p.tiles * ((p.RT + 63) / 64);
+}
 
 // The launch shape, searched over the K split (NS slices of NSB 4-chunk units), the row tiles
 // (NR groups of ITER steps) and the pipeline depth DU (a divisor of the units per wavefront).
@@ -607,7 +618,12 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   m.epi = epi;
   m.oq = QXOut{};
   m.oq_norm = nullptr;
+  m.arg_part = nullptr;
   if (qout) { m.oq = out->q; m.oq_norm = out->norm_w; }
+  if (out && out->arg_part) {
+    if (n != 1) return hipErrorInvalidValue;
+    m.arg_part = out->arg_part;
+  }
   if (other == Q6_K) return launch_t<CQ4K, CQ6K, false>(s, m, p);  // w0 is Q4_K
   if (other == Q4_K) return launch_t<CQ6K, CQ4K, false>(s, m, p);
   switch (w0.type) {

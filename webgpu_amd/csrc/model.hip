@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "internal.h"
+#include "decode.h"
 #include "attention.h"
 #include "matvec.h"
 #include "model.h"
@@ -63,6 +64,7 @@ struct wgd_model {
   StepState *state = nullptr;
   int32_t *tokens = nullptr;    // decode output ring, one per position
   int32_t *argmax_buf = nullptr;
+  uint64_t *arg_part = nullptr; uint32_t arg_entries = 0;  // head argmax keys (quantized path)
   float *att_part = nullptr; uint64_t att_part_floats = 0;
   bool use_graph = true;         // WGD_GRAPH=0 disables capture (profilers, debugging)
   // Quantized-activation decode path (every matrix Q4_K, Q6_K or Q8_0): activation buffers
@@ -213,6 +215,28 @@ __global__ void k_advance(StepState *st, const int32_t *arg, int32_t *tokens, ui
   st->step += 1;
 }
 
+// The greedy pick from the head matvec's per-wavefront argmax keys (first index of the
+// finite maximum; -1 when no logit is finite), then, with `advance`, the k_advance update.
+__global__ __launch_bounds__(256) void k_argmax_advance(const uint64_t *part, uint32_t np, int32_t *out, StepState *st,
+                                                        int32_t *tokens, uint32_t cap, int advance) {
+  __shared__ uint64_t red[4];
+  uint64_t k = 0;
+  for (uint32_t i = threadIdx.x; i < np; i += 256) k = key_max(k, part[i]);
+  k = wave_max_key(k);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  const uint64_t mk = key_max(key_max(red[0], red[1]), key_max(red[2], red[3]));
+  int32_t t = mk ? (int32_t)(0xFFFFFFFFu - (uint32_t)mk) : -1;
+  *out = t;
+  if (!advance) return;
+  if (t < 0) { st->error = 1; t = 0; }
+  if ((uint32_t)st->step < cap) tokens[st->step] = t;
+  st->token = t;
+  st->pos += 1;
+  st->step += 1;
+}
+
 QXView qv(void *p, uint32_t K, bool normed = false, float eps = 0.f) { return qx_const(qx_view(p, K), K, normed, eps); }
 
 // Matvecs of several matrices that read the same activation: one launch for K-quants
@@ -302,14 +326,12 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
     }
   }
   const Matrix &W = m->have_output && !c.tied_output ? m->output : m->embd;
-  WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H, true, c.epsilon), m->logits, MV_STORE));
-  WGD_HIP(argmax(s, m->logits, c.vocab, m->argmax_buf));
-  if (advance) {
-    hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, m->state, (const int32_t *)m->argmax_buf, m->tokens,
-                       (uint32_t)m->c.context);
-    WGD_HIP(hipGetLastError());
-  }
-  return hipSuccess;
+  MVOut hout;
+  hout.arg_part = m->arg_part;
+  WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H, true, c.epsilon), m->logits, MV_STORE, &hout));
+  hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(256), 0, s, (const uint64_t *)m->arg_part, m->arg_entries,
+                     m->argmax_buf, m->state, m->tokens, (uint32_t)m->c.context, advance ? 1 : 0);
+  return hipGetLastError();
 }
 
 // One decode step with n = 1 for models whose matrices the quantized matvec does not read
@@ -568,6 +590,8 @@ int wgd_model_ready(wgd_model *m) {
     rc = rc ? rc : alloc(m, qx_bytes(qd), "qx o", &m->qx_o);
     rc = rc ? rc : alloc(m, qx_bytes(F), "qx down", &m->qx_down);
     rc = rc ? rc : alloc(m, qx_bytes(H), "qx head", &m->qx_head);
+    m->arg_entries = mv_arg_entries(head_w);
+    rc = rc ? rc : alloc_t(m, m->arg_entries, "head argmax keys", &m->arg_part);
     if (rc) return rc;
     m->qpath = true;
     const bool norms = !(is_gemma(m) || c.qk_norm) || [&] {
