@@ -84,51 +84,59 @@ __device__ __forceinline__ uint4 bl16c(Rsrc r, uint32_t v) {
 __device__ __forceinline__ uint32_t bl4c(Rsrc r, uint32_t v) { return __builtin_amdgcn_raw_buffer_load_b32(r, v, 0, 0); }
 __device__ __forceinline__ float f16lo(uint32_t v) { return __half2float(__ushort_as_half((unsigned short)(v & 0xFFFFu))); }
 
+__device__ __forceinline__ float f16hi(uint32_t v) { return __half2float(__ushort_as_half((unsigned short)(v >> 16))); }
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
 }
 
-// Per-unit position: tile T (16 rows) and the first of the 4 chunk columns.
+// Digit sums of one MFMA output lane -> f32: s0 * 254^2 + s1 * 254 + s2. For 4-bit weights
+// the weighted sum is exact in int32 (|s0| <= 16 * 15 * 127); wider weights form the first
+// two digits in integers and the last step in f32.
+__device__ __forceinline__ float dig4(v4i d) { return (float)(__mul24(d[0], 64516) + __mul24(d[1], 254) + d[2]); }
+__device__ __forceinline__ float dig8(v4i d) { return fmaf((float)(__mul24(d[0], 254) + d[1]), 254.f, (float)d[2]); }
+
+// One unit: tile T (16 rows) and the first of its 8 chunk columns (cb % 8 == 0). A lane
+// (row r, group g) takes columns cb + g and cb + 4 + g: for the K-quants the two sub-blocks
+// g and 4 + g of one 256-element block, so its scale fields are at lane-constant bit offsets.
 struct Unit { uint32_t T, cb; };
 
-// Activation of a lane's chunk for one unit, read from LDS: the A operands (block-diagonal
-// digits) and the block scales (already divided by 254^2) and sums of the chunk.
-struct XA { v4i a[2]; float s[2], m[2]; };
+// Activation of a lane's two chunk columns, read from LDS: per column the A operands of its
+// 16-element K-groups (block-diagonal digits) and, per 16 elements, the block scale (divided
+// by 254^2) and the exact block sum.
+struct XA { v4i a[2][2]; float s[2][2], m[2][2]; };
+
+constexpr uint32_t M4 = 0x0F0F0F0Fu;
 
 // Q4_K: chunk byte i = q[i] | q[i + 16] << 4; header plane: the GGUF header (d, dmin, 12
-// bytes of packed 6-bit scales/mins, quant.ts:10-16).
+// bytes of packed 6-bit scales/mins, quant.ts:10-16). Sub-block g: scale and min are the
+// low 6 bits of header bytes 4 + g and 8 + g; sub-block 4 + g: low 4 bits of byte 12 + g
+// (scale) and its high 4 bits (min), top 2 bits from bytes 4 + g and 8 + g.
 struct CQ4K {
-  static constexpr int N = 32, NA = 2;
-  struct W { uint4 q, h; };
-  // Lane constants: load offsets and the scale/min unpack of sub-block j = g (even quads,
-  // packed scales 0-3: bytes 4 + j and 8 + j, 6 bits) or j = 4 + g (odd quads: low 4 bits
-  // in byte 12 + g, high 2 bits in bytes 4 + g and 8 + g).
-  struct L { uint32_t vq, vh, s6, s4, sh, sm; };
-  static __device__ __forceinline__ L lane(uint32_t r, uint32_t g) {
-    return L{256 * g + 16 * r, 16 * r, 8 * g, 8 * g, 8 * g + 6, 8 * g + 4};
-  }
+  static constexpr int N = 32;
+  struct W { uint4 q0, q1, h; };
+  struct L { uint32_t vq, vh, g8; };
+  static __device__ __forceinline__ L lane(uint32_t r, uint32_t g) { return L{256 * g + 16 * r, 16 * r, 8 * g}; }
   static __device__ __forceinline__ W load(Rsrc w, const MVSeg &s, uint32_t C, const Unit &u, const L &l) {
     W r;
-    r.q = bl16(w, l.vq, 256 * (u.T * C + u.cb));
+    const uint32_t so = 256 * (u.T * C + u.cb);
+    r.q0 = bl16(w, l.vq, so);
+    r.q1 = bl16(w, l.vq + 1024, so);
     r.h = bl16(w, l.vh, s.nbp * 128 + 256 * (u.T * s.bpr + u.cb / 8));
     return r;
   }
-  static __device__ __forceinline__ float dot(const W &r, const L &l, const XA &x, uint32_t cb) {
-    const v4i blo = {(int)(r.q.x & 0x0F0F0F0Fu), (int)(r.q.y & 0x0F0F0F0Fu), (int)(r.q.z & 0x0F0F0F0Fu), (int)(r.q.w & 0x0F0F0F0Fu)};
-    const v4i bhi = {(int)((r.q.x >> 4) & 0x0F0F0F0Fu), (int)((r.q.y >> 4) & 0x0F0F0F0Fu), (int)((r.q.z >> 4) & 0x0F0F0F0Fu),
-                     (int)((r.q.w >> 4) & 0x0F0F0F0Fu)};
-    const v4i dl = mfma_i8(x.a[0], blo), dh = mfma_i8(x.a[1], bhi);
-    // digit sums of 16 4-bit weights fit int32 weighted by 254^2, 254, 1 (|d0 sum| <= 16 * 15 * 127)
-    const int tl = __mul24(dl[0], 64516) + __mul24(dl[1], 254) + dl[2];
-    const int th = __mul24(dh[0], 64516) + __mul24(dh[1], 254) + dh[2];
-    // both packings, selected by the (uniform) quad parity: no branch in the unit's code
-    const uint32_t sce = __builtin_amdgcn_ubfe(r.h.y, l.s6, 6), mne = __builtin_amdgcn_ubfe(r.h.z, l.s6, 6);
-    const uint32_t sco = __builtin_amdgcn_ubfe(r.h.w, l.s4, 4) | (__builtin_amdgcn_ubfe(r.h.y, l.sh, 2) << 4);
-    const uint32_t mno = __builtin_amdgcn_ubfe(r.h.w, l.sm, 4) | (__builtin_amdgcn_ubfe(r.h.z, l.sh, 2) << 4);
-    const bool odd = (cb & 4) != 0;
-    const uint32_t sc = odd ? sco : sce, mn = odd ? mno : mne;
-    const float S_ = x.s[0] * (float)tl + x.s[1] * (float)th;
-    return f16lo(r.h.x) * (float)sc * S_ - f16lo(r.h.x >> 16) * (float)mn * (x.m[0] + x.m[1]);
+  static __device__ __forceinline__ float chunk(const uint4 &q, const v4i (&a)[2], const float (&sx)[2]) {
+    const v4i lo = {(int)(q.x & M4), (int)(q.y & M4), (int)(q.z & M4), (int)(q.w & M4)};
+    const v4i hi = {(int)((q.x >> 4) & M4), (int)((q.y >> 4) & M4), (int)((q.z >> 4) & M4), (int)((q.w >> 4) & M4)};
+    return fmaf(sx[1], dig4(mfma_i8(a[1], hi)), sx[0] * dig4(mfma_i8(a[0], lo)));
+  }
+  static __device__ __forceinline__ float dot(const W &r, const L &l, const XA &x) {
+    const float ca = chunk(r.q0, x.a[0], x.s[0]), cb = chunk(r.q1, x.a[1], x.s[1]);
+    const uint32_t sca = __builtin_amdgcn_ubfe(r.h.y, l.g8, 6), mna = __builtin_amdgcn_ubfe(r.h.z, l.g8, 6);
+    const uint32_t scb = __builtin_amdgcn_ubfe(r.h.w, l.g8, 4) | (__builtin_amdgcn_ubfe(r.h.y, l.g8 + 6, 2) << 4);
+    const uint32_t mnb = __builtin_amdgcn_ubfe(r.h.w, l.g8 + 4, 4) | (__builtin_amdgcn_ubfe(r.h.z, l.g8 + 6, 2) << 4);
+    const float u = fmaf((float)scb, cb, (float)sca * ca);
+    const float v = fmaf((float)mnb, x.m[1][0] + x.m[1][1], (float)mna * (x.m[0][0] + x.m[0][1]));
+    return fmaf(f16lo(r.h.x), u, -f16hi(r.h.x) * v);
   }
 };
 
@@ -136,55 +144,61 @@ struct CQ4K {
 // elements 8m+b, 16+8m+b, 8m+4+b, 16+8m+4+b at bits 0, 2, 4, 6; two int8 scales per chunk
 // (one per 16 elements) and the block's f16 d in their planes (quant.ts:21-27).
 struct CQ6K {
-  static constexpr int N = 32, NA = 2;
-  struct W { uint4 q; uint2 h; uint32_t s, d; };
+  static constexpr int N = 32;
+  struct W { uint4 q0, q1; uint2 h0, h1; uint32_t s0, s1, d; };
   struct L { uint32_t vq, vh, vs, vd; };
   static __device__ __forceinline__ L lane(uint32_t r, uint32_t g) { return L{256 * g + 16 * r, 128 * g + 8 * r, 32 * g + 2 * r, 2 * r}; }
   static __device__ __forceinline__ W load(Rsrc w, const MVSeg &s, uint32_t C, const Unit &u, const L &l) {
     W r;
     const uint32_t tc = u.T * C + u.cb;
-    r.q = bl16(w, l.vq, 256 * tc);
-    r.h = bl8(w, l.vh, s.nbp * 128 + 128 * tc);
-    r.s = bl2(w, l.vs, s.nbp * 192 + 32 * tc);
+    r.q0 = bl16(w, l.vq, 256 * tc);
+    r.q1 = bl16(w, l.vq + 1024, 256 * tc);
+    r.h0 = bl8(w, l.vh, s.nbp * 128 + 128 * tc);
+    r.h1 = bl8(w, l.vh + 512, s.nbp * 128 + 128 * tc);
+    r.s0 = bl2(w, l.vs, s.nbp * 192 + 32 * tc);
+    r.s1 = bl2(w, l.vs + 128, s.nbp * 192 + 32 * tc);
     r.d = bl2(w, l.vd, s.nbp * 208 + 32 * (u.T * s.bpr + u.cb / 8));
     return r;
   }
-  static __device__ __forceinline__ float dot(const W &r, const L &, const XA &x, uint32_t) {
-    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+  static __device__ __forceinline__ float chunk(const uint4 &qq, const uint2 &h, uint32_t sc, const v4i (&a)[2],
+                                                const float (&sx)[2], const float (&mx)[2]) {
+    const uint32_t q[4] = {qq.x, qq.y, qq.z, qq.w};
     v4i blo, bhi;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const uint32_t Q = (k < 2 ? r.h.x : r.h.y) >> (4 * (k & 1));
-      blo[k] = (int)((q[k] & 0x0F0F0F0Fu) | ((Q << 4) & 0x30303030u));
-      bhi[k] = (int)(((q[k] >> 4) & 0x0F0F0F0Fu) | ((Q << 2) & 0x30303030u));
+      const uint32_t Q = (k < 2 ? h.x : h.y) >> (4 * (k & 1));
+      blo[k] = (int)((q[k] & M4) | ((Q << 4) & 0x30303030u));
+      bhi[k] = (int)(((q[k] >> 4) & M4) | ((Q << 2) & 0x30303030u));
     }
-    const v4i dl = mfma_i8(x.a[0], blo), dh = mfma_i8(x.a[1], bhi);
-    // 6-bit sums overflow the 254^2 weighting: first two digits in integers
-    const float cl = (float)(__mul24(dl[0], 254) + dl[1]) * 254.f + (float)dl[2];
-    const float ch = (float)(__mul24(dh[0], 254) + dh[1]) * 254.f + (float)dh[2];
-    const float s0 = (float)(int8_t)(r.s & 0xFFu), s1 = (float)(int8_t)((r.s >> 8) & 0xFFu);
-    return f16lo(r.d) * (s0 * (x.s[0] * cl - 32.f * x.m[0]) + s1 * (x.s[1] * ch - 32.f * x.m[1]));
+    const float cl = dig8(mfma_i8(a[0], blo)), ch = dig8(mfma_i8(a[1], bhi));
+    const float s0 = (float)(int8_t)(sc & 0xFFu), s1 = (float)(int8_t)((sc >> 8) & 0xFFu);
+    return fmaf(s1, fmaf(sx[1], ch, -32.f * mx[1]), s0 * fmaf(sx[0], cl, -32.f * mx[0]));
+  }
+  static __device__ __forceinline__ float dot(const W &r, const L &, const XA &x) {
+    return f16lo(r.d) * (chunk(r.q0, r.h0, r.s0, x.a[0], x.s[0], x.m[0]) + chunk(r.q1, r.h1, r.s1, x.a[1], x.s[1], x.m[1]));
   }
 };
 
 // Q8_0: a chunk is half a block, 16 int8 quants (already MFMA operands); d per block
-// (quant.ts:8).
+// (quant.ts:8). A unit is four blocks per row; a lane's columns cb + g and cb + 4 + g are in
+// blocks cb / 2 + g / 2 and two after it.
 struct CQ80 {
-  static constexpr int N = 16, NA = 1;
-  struct W { uint4 q; uint32_t d; };
+  static constexpr int N = 16;
+  struct W { uint4 q0, q1; uint32_t d0, d1; };
   struct L { uint32_t vq, vd; };
   static __device__ __forceinline__ L lane(uint32_t r, uint32_t g) { return L{256 * g + 16 * r, 32 * (g >> 1) + 2 * r}; }
   static __device__ __forceinline__ W load(Rsrc w, const MVSeg &s, uint32_t C, const Unit &u, const L &l) {
     W r;
-    r.q = bl16(w, l.vq, 256 * (u.T * C + u.cb));
-    r.d = bl2(w, l.vd, s.nbp * 32 + 32 * (u.T * s.bpr + u.cb / 2));
+    const uint32_t so = 256 * (u.T * C + u.cb), sd = s.nbp * 32 + 32 * (u.T * s.bpr + u.cb / 2);
+    r.q0 = bl16(w, l.vq, so);
+    r.q1 = bl16(w, l.vq + 1024, so);
+    r.d0 = bl2(w, l.vd, sd);
+    r.d1 = bl2(w, l.vd + 64, sd);
     return r;
   }
-  static __device__ __forceinline__ float dot(const W &r, const L &, const XA &x, uint32_t) {
-    const v4i b = {(int)r.q.x, (int)r.q.y, (int)r.q.z, (int)r.q.w};
-    const v4i d = mfma_i8(x.a[0], b);
-    const float c = (float)(__mul24(d[0], 254) + d[1]) * 254.f + (float)d[2];
-    return f16lo(r.d) * x.s[0] * c;
+  static __device__ __forceinline__ float dot(const W &r, const L &, const XA &x) {
+    const v4i b0 = {(int)r.q0.x, (int)r.q0.y, (int)r.q0.z, (int)r.q0.w}, b1 = {(int)r.q1.x, (int)r.q1.y, (int)r.q1.z, (int)r.q1.w};
+    return fmaf(f16lo(r.d1) * x.s[1][0], dig8(mfma_i8(x.a[1][0], b1)), f16lo(r.d0) * x.s[0][0] * dig8(mfma_i8(x.a[0][0], b0)));
   }
 };
 
@@ -231,16 +245,16 @@ __device__ __forceinline__ float finish_row(const MV &m, const MVSeg &g, uint32_
   return out;
 }
 
-// LDS (dynamic): [0, 32) zeros | digit planes p at 32 + p * ke | block scales / 254^2 and sums
-// (ke / 16 floats each) | partial sums [NS][RT][4 groups] (two sets for a gated pair) | 16
-// floats of reduction scratch.
-struct LdsMap { uint32_t digits, scale, sum, vals, vals1, red, bytes; };
+// LDS (dynamic): [0, 256) zeros (the A operand reads of off-diagonal lanes) | digit planes p
+// at 256 + p * ke | per 16-element block {scale / 254^2, sum} (ke / 16 float pairs) | partial
+// sums [NS][RT][4 groups] (two sets for a gated pair) | 16 floats of reduction scratch.
+constexpr uint32_t MV_ZERO = 256;
+struct LdsMap { uint32_t digits, sm, vals, vals1, red, bytes; };
 __host__ __device__ inline LdsMap lds_map(uint32_t ke, uint32_t ns, uint32_t rt, bool glu) {
   LdsMap l;
-  l.digits = 32;
-  l.scale = 32 + 3 * ke;
-  l.sum = l.scale + 4 * (ke / 16);
-  l.vals = l.sum + 4 * (ke / 16);
+  l.digits = MV_ZERO;
+  l.sm = MV_ZERO + 3 * ke;
+  l.vals = l.sm + 8 * (ke / 16);
   l.vals1 = l.vals + 16 * ns * rt;
   l.red = l.vals1 + (glu ? 16 * ns * rt : 0);
   l.bytes = l.red + 64;
@@ -259,12 +273,12 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   const uint32_t row0 = t * m.RT, tile0 = row0 / 16;
   const uint32_t r = lane & 15, gq = lane >> 4;
   const typename T::L lc = T::lane(r, gq);
-  // unit u of this wavefront: step u / NSB (tile tile0 + rg + step * NR), quad (s * NSB + u % NSB)
+  // unit u of this wavefront: step u / NSB (tile tile0 + rg + step * NR), octet (s * NSB + u % NSB)
   // (uniform: readfirstlane keeps the load offsets in SGPRs whatever the divergence analysis
   // concludes about the loop counters)
   auto unit_of = [&](uint32_t step, uint32_t sl) -> Unit {
     return Unit{(uint32_t)__builtin_amdgcn_readfirstlane(tile0 + rg + step * m.NR),
-                (uint32_t)__builtin_amdgcn_readfirstlane(4 * (s * m.NSB + sl))};
+                (uint32_t)__builtin_amdgcn_readfirstlane(8 * (s * m.NSB + sl))};
   };
   typename T::W buf[DU], buf1[GLU ? DU : 1];
   uint32_t is_step = 0, is_sl = 0;  // next unit to issue
@@ -308,7 +322,7 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
 #pragma unroll
   for (int d = 0; d < DU; d++) issue(d);
   __builtin_amdgcn_sched_barrier(0);
-  if (tid < 2) *(uint4 *)(lds + 16 * tid) = make_uint4(0, 0, 0, 0);
+  if (tid < MV_ZERO / 16) *(uint4 *)(lds + 16 * tid) = make_uint4(0, 0, 0, 0);
 #pragma unroll
   for (uint32_t j = 0; j < XJ; j++) {
     const uint32_t e = (tid + j * nt) * 16;
@@ -320,18 +334,14 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
 #pragma unroll
   for (uint32_t j = 0; j < XB; j++) {
     const uint32_t i = tid + j * nt;
-    if (i < blocks) {
-      ((float *)(lds + L.scale))[i] = __uint_as_float(xsc[j]) * (1.f / 64516.f);
-      ((float *)(lds + L.sum))[i] = __uint_as_float(xsm[j]);
-    }
+    if (i < blocks) *(float2 *)(lds + L.sm + 8 * i) = make_float2(__uint_as_float(xsc[j]) * (1.f / 64516.f), __uint_as_float(xsm[j]));
     ss += __uint_as_float(xsq[j]);
   }
   for (uint32_t e = (tid + XJ * nt) * 16; e < m.ke; e += nt * 16)
 #pragma unroll
     for (int p = 0; p < 3; p++) *(uint4 *)(lds + L.digits + p * m.ke + e) = bl16c(rxd[p], e);
   for (uint32_t i = tid + XB * nt; i < blocks; i += nt) {
-    ((float *)(lds + L.scale))[i] = __uint_as_float(bl4c(rxs, 4 * i)) * (1.f / 64516.f);
-    ((float *)(lds + L.sum))[i] = __uint_as_float(bl4c(rxm, 4 * i));
+    *(float2 *)(lds + L.sm + 8 * i) = make_float2(__uint_as_float(bl4c(rxs, 4 * i)) * (1.f / 64516.f), __uint_as_float(bl4c(rxm, 4 * i)));
     ss += __uint_as_float(bl4c(rxq, 4 * i));
   }
   if (m.x.normed) {
@@ -340,10 +350,12 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   }
   __syncthreads();
   // per-lane LDS addresses of the A operands: diagonal lanes read digit p = r % 4 of their
-  // group's elements, the others the zero line
+  // group's elements, the others the zero line (the unit's reads stay below MV_ZERO); the
+  // unit's offsets from the address are immediates
   const bool diag = (r >> 2) == gq && (r & 3) < 3;
   const uint32_t amask = diag ? 0xFFFFFFFFu : 0u;
   const uint32_t abase = L.digits + (r & 3) * m.ke + T::N * gq;
+  const uint32_t smbase = L.sm + (T::N == 32 ? 16 * gq : 8 * gq);
   // Units are computed in chunks of DU (DU divides NSB, so a chunk never straddles a row
   // step); the per-unit code has no branches, so the compiler can overlap the LDS reads and
   // MFMAs of a chunk's units. A step's partial sums go to LDS after its last chunk.
@@ -352,19 +364,29 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   auto compute = [&](int slot, uint32_t sl) {
     const Unit u = unit_of(cs_step, sl);
     XA xa;
-    const uint32_t ad = (abase + T::N * u.cb) & amask;
-    xa.a[0] = *(const v4i *)(lds + ad);
-    if (T::NA == 2) xa.a[1] = *(const v4i *)(lds + ((ad + 16) & amask));
-    const uint32_t c = u.cb + gq;
+    const uint8_t *ad = lds + ((abase + T::N * u.cb) & amask);
     if (T::N == 32) {
-      const float2 sc = *(const float2 *)(lds + L.scale + 8 * c), sm = *(const float2 *)(lds + L.sum + 8 * c);
-      xa.s[0] = sc.x; xa.s[1] = sc.y; xa.m[0] = sm.x; xa.m[1] = sm.y;
+      // columns cb + g and cb + 4 + g: 32 digits each, two 16-element blocks each
+      xa.a[0][0] = *(const v4i *)(ad);
+      xa.a[0][1] = *(const v4i *)(ad + 16);
+      xa.a[1][0] = *(const v4i *)(ad + 128);
+      xa.a[1][1] = *(const v4i *)(ad + 144);
+      const float4 s0 = *(const float4 *)(lds + smbase + 8 * 2 * u.cb);
+      const float4 s1 = *(const float4 *)(lds + smbase + 8 * 2 * u.cb + 64);
+      xa.s[0][0] = s0.x; xa.m[0][0] = s0.y; xa.s[0][1] = s0.z; xa.m[0][1] = s0.w;
+      xa.s[1][0] = s1.x; xa.m[1][0] = s1.y; xa.s[1][1] = s1.z; xa.m[1][1] = s1.w;
     } else {
-      xa.s[0] = ((const float *)(lds + L.scale))[c];
-      xa.m[0] = 0.f;
+      // 16-element columns cb + g and cb + 4 + g
+      xa.a[0][0] = *(const v4i *)(ad);
+      xa.a[1][0] = *(const v4i *)(ad + 64);
+      xa.a[0][1] = xa.a[1][1] = v4i{0, 0, 0, 0};
+      const float2 s0 = *(const float2 *)(lds + smbase + 8 * u.cb);
+      const float2 s1 = *(const float2 *)(lds + smbase + 8 * u.cb + 32);
+      xa.s[0][0] = s0.x; xa.m[0][0] = s0.y; xa.s[1][0] = s1.x; xa.m[1][0] = s1.y;
+      xa.s[0][1] = xa.s[1][1] = xa.m[0][1] = xa.m[1][1] = 0.f;
     }
-    acc += T::dot(buf[slot], lc, xa, u.cb);
-    if (GLU) acc1 += T::dot(buf1[slot], lc, xa, u.cb);
+    acc += T::dot(buf[slot], lc, xa);
+    if (GLU) acc1 += T::dot(buf1[slot], lc, xa);
   };
   auto chunk_done = [&]() {
     cs_sl += DU;
@@ -483,28 +505,31 @@ uint32_t mv_arg_entries(const Matrix &w) {
   return p.tiles * ((p.RT + 63) / 64);
 }
 
-// The launch shape, searched over the K split (NS slices of NSB 4-chunk units), the row tiles
-// (NR groups of ITER steps) and the pipeline depth DU (a divisor of the units per wavefront).
-// The cost is the rows the busiest CU streams (whole rounds of CU-count tiles), stretched
-// when a CU holds less than ~48 KB of loads in flight, when the activation staging is
-// amortised over few rows, and for idle chunk columns.
+// The launch shape, searched over the K split (NS slices of NSB 8-column units), the row
+// tiles (NR groups of ITER steps) and the pipeline depth DU (a divisor of the units per
+// wavefront). The cost is the rows the busiest CU streams (whole rounds of CU-count tiles),
+// stretched when a CU holds less than ~64 KB of weight loads in flight (more than ~100 KB
+// only queues), when the activation staging is amortised over few rows, and for idle chunk
+// columns.
 MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out) {
   MVPlan best_p{};
-  const uint32_t N = chunk_elems(w.type), C = w.cols / N, CQ = (C + 3) / 4;
+  const uint32_t N = chunk_elems(w.type), C = w.cols / N, CQ = (C + 7) / 8;
   const uint32_t cus = (uint32_t)device_cu_count();
   static const int env_ns = getenv("WGD_MV_NS") ? atoi(getenv("WGD_MV_NS")) : 0;
   static const int env_iter = getenv("WGD_MV_ITER") ? atoi(getenv("WGD_MV_ITER")) : 0;
   static const int env_nr = getenv("WGD_MV_NR") ? atoi(getenv("WGD_MV_NR")) : 0;
   static const int env_du = getenv("WGD_MV_DU") ? atoi(getenv("WGD_MV_DU")) : 0;
-  const uint32_t dumax = glu ? 4 : 8;
+  const uint32_t dumax = glu ? 2 : 4;
+  // unique weight bytes of one unit (16 rows x 8 chunk columns and its scale planes), KB
+  const double unit_kb = w.type == Q6_K ? 2.625 : w.type == Q4_K ? 2.25 : 2.125;
   double best_cost = 1e30;
   for (uint32_t ns = 1; ns <= 16; ns++) {
     if (env_ns && (int)ns != env_ns) continue;
     const uint32_t nsb = (CQ + ns - 1) / ns;
     if ((nsb - 1) * ns >= CQ && ns > 1) continue;  // a slice would be empty
-    const uint32_t waste = ns * nsb * 4 - C;
+    const uint32_t waste = ns * nsb * 8 - C;
     if (waste * 7 > C && ns > 1) continue;
-    const uint32_t ke = ns * nsb * 4 * N;
+    const uint32_t ke = ns * nsb * 8 * N;
     for (uint32_t nr = 1; nr * ns <= 16; nr++) {
       if (env_nr && (int)nr != env_nr) continue;
       for (uint32_t iter = 1; iter <= 256; iter++) {
@@ -515,20 +540,21 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
         const LdsMap lm = lds_map(ke, ns, rt, glu);
         if (lm.bytes > lds_limit()) break;
         const uint32_t units = iter * nsb;
-        uint32_t du = dumax;  // a chunk of DU units stays within one row step
-        while (du > 1 && nsb % du) du /= 2;
-        if (env_du) { if (nsb % (uint32_t)env_du || (uint32_t)env_du > dumax) continue; du = (uint32_t)env_du; }
         uint32_t tiles = 0;
         for (uint32_t i = 0; i < n; i++) tiles += (rows[i] + rt - 1) / rt;
         const uint32_t rounds = (tiles + cus - 1) / cus;
-        // Little's law: a CU streams at full share with ~48 KB of loads in flight; each unit
-        // load of a wavefront is 1 KB (16 rows x 4 chunks)
         const uint32_t per_cu = lm.bytes > 80 * 1024 ? 1 : 2;
         const double resident = tiles >= per_cu * cus ? (double)per_cu : tiles > cus ? (double)tiles / cus : 1.0;
-        const double inflight = (double)(nr * ns) * (units < du ? units : du) * (glu ? 2 : 1) * resident;
+        auto inflight = [&](uint32_t du) {
+          return (double)(nr * ns) * (units < du ? units : du) * (glu ? 2 : 1) * unit_kb * resident;
+        };
+        // deepest pipeline (a divisor of NSB, so a window of DU units stays in one row step)
+        // that keeps a CU's loads in flight within ~100 KB
+        uint32_t du = dumax;
+        while (du > 1 && (nsb % du || inflight(du) > 100.0)) du /= 2;
+        if (env_du) { if (nsb % (uint32_t)env_du || (uint32_t)env_du > dumax) continue; du = (uint32_t)env_du; }
         double cost = (double)rounds * rt * (1.0 + (double)waste / C);
-        if (inflight < 48.0) cost *= 48.0 / inflight;
-        if (units > du) cost *= 1.0 + 0.1 * (dumax / du - 1);
+        if (inflight(du) < 64.0) cost *= 64.0 / inflight(du);
         cost *= 1.0 + 2.0 / rt;  // activation staging per workgroup
         if (cost < best_cost) {
           best_cost = cost;
@@ -559,8 +585,7 @@ static hipError_t launch_t(hipStream_t s, const MV &m, const MVPlan &p) {
   switch (p.DU) {
     case 1: return go(k_mv<T0, T1, 1, GLU>);
     case 2: return go(k_mv<T0, T1, 2, GLU>);
-    case 4: return go(k_mv<T0, T1, 4, GLU>);
-    case 8: if constexpr (!GLU) return go(k_mv<T0, T1, 8, GLU>); else break;
+    case 4: if constexpr (!GLU) return go(k_mv<T0, T1, 4, GLU>); else break;
   }
   return hipErrorInvalidValue;
 }
@@ -613,7 +638,7 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   }
   m.x = x;
   m.C = p.C;
-  m.ke = p.NS * p.NSB * 4 * chunk_elems(w0.type);
+  m.ke = p.NS * p.NSB * 8 * chunk_elems(w0.type);
   m.NS = p.NS; m.NSB = p.NSB; m.NR = p.NR; m.ITER = p.ITER; m.RT = p.RT; m.U = p.ITER * p.NSB;
   m.epi = epi;
   m.oq = QXOut{};
