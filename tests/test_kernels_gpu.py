@@ -123,6 +123,27 @@ def test_prompt_gemm_on_mfma(gpu, type_):
             gpu.destroy(buf)
 
 
+@pytest.mark.parametrize("type_,rows,cols,batch", [(Q4_K, 4096, 4096, 128), (Q6_K, 1024, 4096, 130),
+                                                   (Q8_0, 384, 2048, 128), (Q4_K, 640, 14336, 64)])
+def test_prompt_gemm_real_shapes(gpu, type_, rows, cols, batch):
+    """Planar prompt GEMM at layer shapes: whole 128-token tiles, a second token tile,
+    split-K partial sums, a row offset inside a wider output (stride/rowBase, verify.ts:16-38)."""
+    rng = np.random.default_rng(rows * 3 + cols + batch)
+    gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+    w = gen(rng, rows * cols // QUANTS[type_]["block"])
+    x = rng.standard_normal((batch + 1) * cols).astype(np.float32)
+    stride, base = rows + 8, 5
+    want = orc.matmul(type_, w, x, cols, rows, stride, base, 1, batch)
+    wb = gpu.upload_weights(type_, cols, rows, w)
+    xb, yb = gpu.upload(x, "x"), gpu.buffer(batch * stride * 4, "y")
+    gpu.matmul(type_, wb, xb, yb, cols, rows, stride, base, 1, batch)
+    y = gpu.read_f32(yb, batch * stride).reshape(batch, stride)
+    want = np.concatenate([want, np.zeros(batch * stride - want.size)]).reshape(batch, stride)
+    near(y[:, base:base + rows].ravel(), want[:, base:base + rows].ravel(), 1e-4, f"gemm {type_} {rows}x{cols}x{batch}")
+    for buf in (wb, xb, yb):
+        gpu.destroy(buf)
+
+
 # ---------------------------------------------------------------- verify.ts:39-54
 @pytest.mark.parametrize("window", [2, 16])
 def test_attention_small(gpu, window):

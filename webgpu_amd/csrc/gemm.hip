@@ -180,9 +180,291 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ planar K-quant GEMM
+//
+// The prompt GEMM of the planar layouts (Q4_K, Q6_K, Q8_0; the decode matvec's weights). A
+// workgroup owns QG_M = 128 weight rows x QG_N = 128 tokens and a K span (split-K when the
+// rows alone give too few workgroups; partial sums are added in split order by
+// k_gemm_reduce, so results do not depend on timing). Per 64-column K tile, every weight
+// of the workgroup's rows is dequantized once, from coalesced 16-byte planar loads (one
+// 32-element chunk of one row per thread), split into bf16 hi + lo and stored in LDS; the
+// activation tile is split the same way. Four wavefronts each compute 64 rows x 64 tokens,
+// sixteen 16 x 16 accumulators, three MFMAs per product (hi*hi + hi*lo + lo*hi). The next
+// K tile's loads are issued before the MFMAs of the current one; 74 KB of LDS lets two
+// workgroups share a CU, so one's dequantization overlaps the other's MFMAs.
+constexpr uint32_t QG_M = 128, QG_N = 128, QG_K = 64, QG_P = QG_K + 8;  // LDS row pitch (bf16)
+constexpr uint32_t QG_LDS = 4 * QG_M * QG_P * 2;  // w hi, w lo, x hi, x lo
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> (hi, lo) bf16 pairs with hi = RN(v), lo = RN(v - hi) (native gfx950 packing).
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  const f32x2 v = {a, b};
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  const f32x2 back = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - back, bf16x2));
+}
+
+struct QGemm {
+  const uint8_t *w; uint32_t wbytes;
+  uint32_t C, bpr, nbp;  // chunk columns, blocks per row, blocks of the padded matrix
+  const float *x; float *y; float *part;
+  uint32_t cols, rows, stride, row_base, input_offset, batch, kspan;
+};
+
+typedef __amdgpu_buffer_rsrc_t QRsrc;
+__device__ __forceinline__ uint4 qld16(QRsrc r, uint32_t off) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// One thread's weights of a K tile: Q4_K / Q6_K one 32-element chunk (row-tile rt, column
+// cc of the tile, row r), Q8_0 two 16-element chunks.
+template <int TYPE> struct QWeights;
+template <> struct QWeights<Q4_K> {
+  uint4 q, h;
+  __device__ void fetch(const QGemm &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+    q = qld16(rw, ((T * a.C + c) * 16 + r) * 16);
+    h = qld16(rw, a.nbp * 128 + ((T * a.bpr + c / 8) * 16 + r) * 16);
+  }
+  // element e < 32 of the chunk into f32 (quant.ts:13-19: d * sc * q - dmin * m)
+  __device__ void values(uint32_t c, float *v) const {
+    const uint32_t s = c & 7, sh = 8 * (s & 3);
+    uint32_t sc, m;
+    if (s < 4) { sc = (h.y >> sh) & 63u; m = (h.z >> sh) & 63u; }
+    else { sc = ((h.w >> sh) & 15u) | (((h.y >> sh) >> 6 & 3u) << 4); m = ((h.w >> sh) >> 4 & 15u) | (((h.z >> sh) >> 6 & 3u) << 4); }
+    const float dsc = half_bits(h.x & 0xFFFFu) * (float)sc, dmm = half_bits(h.x >> 16) * (float)m;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        v[4 * k + b] = fmaf(dsc, (float)((lo >> (8 * b)) & 0xFFu), -dmm);
+        v[16 + 4 * k + b] = fmaf(dsc, (float)((hi >> (8 * b)) & 0xFFu), -dmm);
+      }
+    }
+  }
+};
+template <> struct QWeights<Q6_K> {
+  uint4 q; uint2 qh; uint32_t sc, d;
+  __device__ void fetch(const QGemm &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+    const uint32_t tc = (T * a.C + c) * 16 + r;
+    q = qld16(rw, tc * 16);
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 hv = __builtin_amdgcn_raw_buffer_load_b64(rw, a.nbp * 128 + tc * 8, 0, 0);
+    qh = make_uint2(hv.x, hv.y);
+    sc = __builtin_amdgcn_raw_buffer_load_b16(rw, a.nbp * 192 + tc * 2, 0, 0);
+    d = __builtin_amdgcn_raw_buffer_load_b16(rw, a.nbp * 208 + ((T * a.bpr + c / 8) * 16 + r) * 2, 0, 0);
+  }
+  // quant.ts:21-27: d * scale16 * (q - 32); low nibbles with high bits at bits 4-5
+  __device__ void values(uint32_t, float *v) const {
+    const float d0 = half_bits(d & 0xFFFFu);
+    const float s0 = d0 * (float)(int8_t)(sc & 0xFFu), s1 = d0 * (float)(int8_t)((sc >> 8) & 0xFFu);
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t Q = (k < 2 ? qh.x : qh.y) >> (4 * (k & 1));
+      const uint32_t lo = (qw[k] & 0x0F0F0F0Fu) | ((Q << 4) & 0x30303030u);
+      const uint32_t hi = ((qw[k] >> 4) & 0x0F0F0F0Fu) | ((Q << 2) & 0x30303030u);
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        v[4 * k + b] = s0 * (float)((int)((lo >> (8 * b)) & 0xFFu) - 32);
+        v[16 + 4 * k + b] = s1 * (float)((int)((hi >> (8 * b)) & 0xFFu) - 32);
+      }
+    }
+  }
+};
+template <> struct QWeights<Q8_0> {
+  uint4 q[2]; uint32_t d[2];
+  // chunks 2c and 2c + 1 (16 elements each, one Q8_0 block): c counts 32-element columns
+  __device__ void fetch(const QGemm &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+#pragma unroll
+    for (int u = 0; u < 2; u++) q[u] = qld16(rw, ((T * a.C + 2 * c + u) * 16 + r) * 16);
+    d[0] = d[1] = __builtin_amdgcn_raw_buffer_load_b16(rw, a.nbp * 32 + ((T * a.bpr + c) * 16 + r) * 2, 0, 0);
+  }
+  __device__ void values(uint32_t, float *v) const {
+    const float dd = half_bits(d[0] & 0xFFFFu);
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const uint32_t qw[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) v[16 * u + 4 * k + b] = dd * (float)(int8_t)((qw[k] >> (8 * b)) & 0xFFu);
+    }
+  }
+};
+
+template <int TYPE>
+__global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t qlds[];
+  uint16_t *wh = qlds, *wl = qlds + QG_M * QG_P, *xh = qlds + 2 * QG_M * QG_P, *xl = qlds + 3 * QG_M * QG_P;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv & 1, wn = wv >> 1;
+  const uint32_t m0 = blockIdx.x * QG_M, n0 = blockIdx.y * QG_N, z = blockIdx.z;
+  const uint32_t kb = z * a.kspan, ke = kb + a.kspan < a.cols ? kb + a.kspan : a.cols;
+  const QRsrc rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int)a.wbytes, 0x00020000);
+  // this thread's staging item: weight row-tile / column / row, and activation token / half
+  const uint32_t wrt = tid >> 5, wcc = (tid >> 4) & 1, wr = tid & 15;
+  const uint32_t xt = tid >> 1, xhf = tid & 1;
+  const bool xlive = n0 + xt < a.batch;
+  const float *xrow = a.x + (uint64_t)(n0 + xt + a.input_offset) * a.cols;
+  QWeights<TYPE> wreg;
+  float4 xr[8];
+  auto fetch = [&](uint32_t k0) {
+    wreg.fetch(a, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc);
+#pragma unroll
+    for (int i = 0; i < 8; i++) xr[i] = xlive ? *(const float4 *)(xrow + k0 + 32 * xhf + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto stage = [&](uint32_t k0) {
+    float v[32];
+    wreg.values(k0 / 32 + wcc, v);
+    uint32_t h[16], l[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) split2(v[2 * i], v[2 * i + 1], h[i], l[i]);
+    uint16_t *dh = wh + (wrt * 16 + wr) * QG_P + 32 * wcc, *dl = wl + (wrt * 16 + wr) * QG_P + 32 * wcc;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      *(uint4 *)(dh + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+      *(uint4 *)(dl + 8 * i) = make_uint4(l[4 * i], l[4 * i + 1], l[4 * i + 2], l[4 * i + 3]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      split2(xr[i].x, xr[i].y, h[2 * i], l[2 * i]);
+      split2(xr[i].z, xr[i].w, h[2 * i + 1], l[2 * i + 1]);
+    }
+    uint16_t *eh = xh + xt * QG_P + 32 * xhf, *el = xl + xt * QG_P + 32 * xhf;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      *(uint4 *)(eh + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+      *(uint4 *)(el + 8 * i) = make_uint4(l[4 * i], l[4 * i + 1], l[4 * i + 2], l[4 * i + 3]);
+    }
+  };
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t ar = wm * 64 + (lane & 15), br = wn * 64 + (lane & 15), kq = 8 * (lane >> 4);
+  fetch(kb);
+  for (uint32_t k0 = kb; k0 < ke; k0 += QG_K) {
+    stage(k0);
+    __syncthreads();
+    if (k0 + QG_K < ke) fetch(k0 + QG_K);  // next tile's loads fly during the MFMAs
+#pragma unroll
+    for (uint32_t ks = 0; ks < QG_K; ks += 32) {
+      bf16x8 Ah[4], Al[4], Bh[4], Bl[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        Ah[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(wh + (ar + 16 * i) * QG_P + ks + kq));
+        Al[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(wl + (ar + 16 * i) * QG_P + ks + kq));
+        Bh[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(xh + (br + 16 * i) * QG_P + ks + kq));
+        Bl[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(xl + (br + 16 * i) * QG_P + ks + kq));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[i], Bh[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[i], Bl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al[i], Bh[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+  }
+  // D layout: lane holds rows 4 * (lane / 16) + e, token lane % 16 of each 16 x 16 tile
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t tok = n0 + wn * 64 + 16 * j + (lane & 15);
+    if (tok >= a.batch) continue;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t row = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+        if (row >= a.rows) continue;
+        if (a.part) a.part[((uint64_t)z * a.batch + tok) * a.rows + row] = acc[i][j][e];
+        else a.y[(uint64_t)tok * a.stride + a.row_base + row] = acc[i][j][e];
+      }
+  }
+}
+
+// y[tok * stride + row_base + row] = sum over splits z (in order) of part[z][tok][row].
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *part, float *y, uint32_t rows, uint32_t batch,
+                                                     uint32_t splits, uint32_t stride, uint32_t row_base) {
+  const uint64_t n = (uint64_t)rows * batch;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (uint32_t z = 0; z < splits; z++) v += part[(uint64_t)z * n + i];
+    const uint32_t tok = (uint32_t)(i / rows), row = (uint32_t)(i % rows);
+    y[(uint64_t)tok * stride + row_base + row] = v;
+  }
+}
+
+static bool qgemm_supported(const Matrix &w) {
+  if (w.layout != LAYOUT_PLANAR) return false;
+  if (w.type == Q4_K || w.type == Q6_K) return w.cols % 256 == 0;
+  return w.type == Q8_0 && w.cols % QG_K == 0;
+}
+
+// K span per workgroup: enough splits for a workgroup per CU, each at least 512 columns
+// (whole 256-column blocks; 64 for Q8_0), and no more partial sums than the scratch holds.
+static uint32_t qgemm_kspan(const Matrix &w, uint32_t batch, uint64_t scratch_floats) {
+  const uint32_t align = w.type == Q8_0 ? QG_K : 256;
+  const uint32_t tiles = ((w.rows + QG_M - 1) / QG_M) * ((batch + QG_N - 1) / QG_N);
+  const uint32_t target = (uint32_t)device_cu_count();
+  uint32_t splits = tiles >= target ? 1 : (target + tiles - 1) / tiles;
+  if (splits > w.cols / 512) splits = w.cols / 512 > 0 ? w.cols / 512 : 1;
+  const uint32_t units = w.cols / align;
+  if (splits > units) splits = units;
+  while (splits > 1 && (uint64_t)splits * batch * w.rows > scratch_floats) splits--;
+  if (splits > 16) splits = 16;
+  const uint32_t per = (units + splits - 1) / splits;
+  return per * align;
+}
+
+uint64_t gemm_split_floats(const Matrix &w, uint32_t batch) {
+  if (!qgemm_supported(w) || !batch) return 0;
+  const uint32_t kspan = qgemm_kspan(w, batch, ~0ull);
+  const uint32_t splits = (w.cols + kspan - 1) / kspan;
+  return splits > 1 ? (uint64_t)splits * batch * w.rows : 0;
+}
+
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                uint32_t row_base, uint32_t input_offset, uint32_t batch) {
+                uint32_t row_base, uint32_t input_offset, uint32_t batch, const GemmScratch &scratch) {
   if (!w.rows || !batch) return hipSuccess;
+  if (qgemm_supported(w)) {
+    const uint64_t wbytes = planar_bytes(w.type, w.cols, w.rows);
+    if (wbytes >= (1ull << 31)) return hipErrorInvalidValue;
+    QGemm q;
+    q.w = w.data; q.wbytes = (uint32_t)wbytes;
+    q.C = w.cols / chunk_elems(w.type); q.bpr = w.cols / block_size(w.type); q.nbp = q.bpr * (uint32_t)tile_rows(w.rows);
+    q.x = x; q.y = y; q.cols = w.cols; q.rows = w.rows; q.stride = stride; q.row_base = row_base;
+    q.input_offset = input_offset; q.batch = batch;
+    q.kspan = qgemm_kspan(w, batch, scratch.p ? scratch.floats : 0);
+    const uint32_t splits = (w.cols + q.kspan - 1) / q.kspan;
+    q.part = splits > 1 ? scratch.p : nullptr;
+    const dim3 grid((w.rows + QG_M - 1) / QG_M, (batch + QG_N - 1) / QG_N, splits);
+    auto go = [&](auto kernel) {
+      static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
+      if (!big) { (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)QG_LDS); big = true; }
+      hipLaunchKernelGGL(kernel, grid, dim3(256), QG_LDS, s, q);
+    };
+    if (w.type == Q4_K) go(k_gemm_q<Q4_K>);
+    else if (w.type == Q6_K) go(k_gemm_q<Q6_K>);
+    else go(k_gemm_q<Q8_0>);
+    WGD_HIP(hipGetLastError());
+    if (splits > 1) {
+      const uint64_t n = (uint64_t)w.rows * batch;
+      uint32_t blocks = (uint32_t)((n + 255) / 256);
+      if (blocks > 4096) blocks = 4096;
+      hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(256), 0, s, (const float *)q.part, y, w.rows, batch, splits,
+                         stride, row_base);
+    }
+    return hipGetLastError();
+  }
   if (w.cols % KT) return hipErrorInvalidValue;
   GemmArgs a;
   a.w = w.data; a.type = w.type; a.layout = w.layout;

@@ -65,14 +65,18 @@ hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *d
 
 // ---------------------------------------------------------------- launchers
 
+// Scratch for the prompt GEMM's split-K partial sums; gemm_split_floats() is what a launch
+// of w over `batch` tokens can use (0: it does not split). Less scratch means fewer splits.
+struct GemmScratch { float *p = nullptr; uint64_t floats = 0; };
+uint64_t gemm_split_floats(const Matrix &w, uint32_t batch);
 // y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]: the
 // generic kernel for small batches of GGUF-layout weights, else the MFMA dequant-GEMM.
 hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                  uint32_t row_base, uint32_t input_offset, uint32_t batch);
+                  uint32_t row_base, uint32_t input_offset, uint32_t batch, const GemmScratch &scratch = GemmScratch());
 hipError_t matmul_generic(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
                           uint32_t row_base, uint32_t input_offset, uint32_t batch);
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                uint32_t row_base, uint32_t input_offset, uint32_t batch);
+                uint32_t row_base, uint32_t input_offset, uint32_t batch, const GemmScratch &scratch = GemmScratch());
 
 hipError_t dequant(hipStream_t s, int type, const uint8_t *w, float *out, uint64_t count);
 hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *ids, float *out,

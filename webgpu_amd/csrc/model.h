@@ -23,6 +23,8 @@ struct wgd_context {
   uint64_t att_partial_floats = 0;
   void *mv_qx = nullptr;              // quantized activation row of wgd_matmul
   uint64_t mv_qx_bytes = 0;
+  float *gemm_part = nullptr;         // split-K partial sums of wgd_matmul's prompt GEMM
+  uint64_t gemm_part_floats = 0;
 };
 
 namespace wgd {

@@ -281,7 +281,19 @@ int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
     if (rc) return rc;
     return ctx_check(ctx, mv(ctx->stream, m, nullptr, qx_const(q, cols, false, 0.f), (float *)y->ptr + row_base, MV_STORE), "matmul");
   }
-  return ctx_check(ctx, matmul(ctx->stream, m, (const float *)x->ptr, (float *)y->ptr, stride, row_base, input_offset, batch), "matmul");
+  // split-K partial sums of the prompt GEMM, grown on demand and kept with the context
+  const uint64_t gp = gemm_split_floats(m, batch);
+  if (gp > ctx->gemm_part_floats) {
+    ctx_free(ctx, ctx->gemm_part);
+    ctx->gemm_part = nullptr; ctx->gemm_part_floats = 0;
+    void *p = nullptr;
+    int rc = ctx_alloc(ctx, gp * 4, "GEMM split sums", &p);
+    if (rc) return rc;
+    ctx->gemm_part = (float *)p; ctx->gemm_part_floats = gp;
+  }
+  GemmScratch gs;
+  gs.p = ctx->gemm_part; gs.floats = ctx->gemm_part_floats;
+  return ctx_check(ctx, matmul(ctx->stream, m, (const float *)x->ptr, (float *)y->ptr, stride, row_base, input_offset, batch, gs), "matmul");
 }
 
 uint64_t wgd_quantized_bytes(uint32_t cols) { return qx_bytes(cols); }
