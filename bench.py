@@ -15,6 +15,10 @@ time. traffic = HBM bytes per launch from the committed rocprofv3 counter summar
 same microbench (profiles/k_mv_matvec_microbench.md). The other microbench shapes (4096x4096,
 4096x14336 Q4_K; 4096x128256 Q6_K) are reported under "matvec".
 
+prefill_gemm: the prompt-batch dequant-GEMM at the 8B layer shapes with 128 tokens, timed
+with HIP events; its MFMA utilisation counts the three bf16 MFMAs per product of the
+hi/lo operand split against the 2.5 PFLOP/s dense bf16 peak.
+
 cpu_baseline: the float64 C oracle (OpenMP over the host cores) decoding the same 8B
 model on a bounded sample (8-token prompt, then as many greedy tokens as fit ~15 s).
 """
@@ -133,6 +137,40 @@ def matvec_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, lau
             "copies": copies}
 
 
+PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA peak, flop/s
+GEMM_SHAPES = [(Q4_K, 4096, 14336, 128), (Q4_K, 14336, 4096, 128), (Q4_K, 4096, 4096, 128), (Q6_K, 4096, 1024, 128)]
+
+
+def gemm_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, batch: int, launches: int = 20) -> dict:
+    """One prompt-batch dequant-GEMM (batch tokens x rows x cols, planar weights) timed with a
+    HIP event pair around `launches` back-to-back calls on the library's stream. Algorithmic
+    flops are 2 * batch * rows * cols; the kernel issues three bf16 MFMAs per product (hi/lo
+    operand split), so its MFMA work is three times that."""
+    rng = np.random.default_rng(cols * 5 + rows)
+    gen = synth.microbench_q4k if type_ == Q4_K else synth.microbench_q6k
+    w = gpu.upload_weights(type_, cols, rows, gen(rng, rows, cols), "gemm w")
+    x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32), "gemm x")
+    y = gpu.buffer(batch * rows * 4, "gemm y")
+    for _ in range(3):
+        gpu.matmul(type_, w, x, y, cols, rows, rows, 0, 0, batch)
+    gpu.done()
+    evs = ev.create(2)
+    times = []
+    for rep in range(3):
+        ev.record(evs[0], gpu.stream)
+        for _ in range(launches):
+            gpu.matmul(type_, w, x, y, cols, rows, rows, 0, 0, batch)
+        ev.record(evs[1], gpu.stream)
+        times.append(ev.elapsed_ms(evs[0], evs[1]) * 1e-3 / launches)
+    ev.destroy(evs)
+    for b in (w, x, y):
+        gpu.destroy(b)
+    t = float(np.mean(times))
+    flops = 2.0 * batch * rows * cols
+    return {"shape": f"{cols}x{rows}", "type": QUANTS[type_]["name"], "batch": batch, "us": t * 1e6,
+            "tflops": flops / t / 1e12, "mfma_tflops": 3 * flops / t / 1e12, "mfma_frac": 3 * flops / t / PEAK_BF16}
+
+
 def cpu_baseline(f: np.ndarray, seconds: float = 15.0) -> dict:
     from oracle import orc
     from webgpu_amd.context import attention_memory
@@ -163,6 +201,7 @@ def main() -> None:
     ap.add_argument("--no-matvec", action="store_true", help="skip the matvec microbench")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the matvec microbench and a 256 MiB device copy (counter calibration), no JSON line")
+    ap.add_argument("--gemm-only", action="store_true", help="only the prompt-GEMM microbench, no JSON line")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the token loop runs on a single MI355X (multi-GPU sharding is a design "
@@ -183,6 +222,15 @@ def main() -> None:
             m = matvec_bench(gpu, ev, *s)
             print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
                   f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+        gpu.dispose()
+        return
+    if a.gemm_only:
+        gpu = Compute().init()
+        ev = Events()
+        for sh in GEMM_SHAPES:
+            g = gemm_bench(gpu, ev, *sh)
+            print(f"[bench] gemm {g['type']} {g['shape']} x {g['batch']} tokens: {g['us']:.1f} us, {g['tflops']:.0f} TFLOP/s "
+                  f"({g['mfma_tflops']:.0f} TFLOP/s of bf16 MFMA, {100 * g['mfma_frac']:.1f}% of peak)", file=sys.stderr, flush=True)
         gpu.dispose()
         return
     context = 1024
@@ -239,6 +287,7 @@ def main() -> None:
         ev = Events()
         shapes = [(Q4_K, 14336, 4096), (Q4_K, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 4096, 128256)]
         mv = [matvec_bench(gpu, ev, *s) for s in shapes]
+        gm = [gemm_bench(gpu, ev, *sh) for sh in GEMM_SHAPES]
         gpu.dispose()
         head = mv[0]
         result["roofline"] = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
@@ -246,9 +295,13 @@ def main() -> None:
                               "kernel": f"k_matvec<Q4K> {head['shape']} (in x out), {head['bytes']} B per launch",
                               "mean_us": head["us"]}
         result["matvec"] = mv
+        result["prefill_gemm"] = gm
         for m in mv:
             print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
                   f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+        for g in gm:
+            print(f"[bench] gemm {g['type']} {g['shape']} x {g['batch']} tokens: {g['us']:.1f} us, {g['tflops']:.0f} TFLOP/s "
+                  f"({100 * g['mfma_frac']:.1f}% of bf16 MFMA peak)", file=sys.stderr, flush=True)
     if not a.no_cpu:
         result["cpu_baseline"] = cpu_baseline(f)
         print(f"[bench] cpu baseline {result['cpu_baseline']['value']:.3f} tok/s", file=sys.stderr, flush=True)
