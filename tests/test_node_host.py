@@ -1,0 +1,95 @@
+"""The Node host over the N-API addon (webgpu_amd/node): the reference's own runtime
+(src/core is TypeScript on Node) driving libwgd.
+
+CPU: the addon loads in Node and exports the engine surface; the Node GGUF parser,
+modelConfig and attentionMemory agree with the Python mirror on the same file. GPU: the
+tiny check:dense model through PagedEngine.load/forward/generate under Node matches the
+float64 oracle (logits within 1e-3 max-relative, identical greedy tokens), as the smoke
+check does through the Python host.
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from webgpu_amd import synth
+from webgpu_amd.gguf import model_config, parse_gguf_header
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ADDON = os.path.join(ROOT, "webgpu_amd", "node", "wgd_napi.node")
+RUNNER = os.path.join(ROOT, "tests", "node", "engine_run.mjs")
+NODE = shutil.which("node")
+
+needs_node = pytest.mark.skipif(NODE is None or not os.path.exists(ADDON), reason="node or the built addon is missing")
+
+
+def run_node(*args, timeout=120):
+    r = subprocess.run([NODE, RUNNER, *map(str, args)], capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+@pytest.fixture(scope="module")
+def tiny_file(tmp_path_factory):
+    f = synth.build("tiny")
+    path = tmp_path_factory.mktemp("gguf") / "tiny.gguf"
+    f.tofile(str(path))
+    return str(path), f
+
+
+@needs_node
+def test_addon_exports_engine_surface():
+    code = f"const a = require({json.dumps(ADDON)}); console.log(JSON.stringify(Object.keys(a).sort()))"
+    r = subprocess.run([NODE, "-e", code], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert json.loads(r.stdout) == sorted(["create", "destroy", "adapterName", "memory", "done", "modelCreate",
+                                           "modelTensor", "modelReady", "modelForward", "modelDecode", "modelDestroy"])
+
+
+@needs_node
+def test_node_gguf_config_matches_python(tiny_file):
+    path, f = tiny_file
+    got = run_node(path, "config")
+    g = parse_gguf_header(f, f.size)
+    c = model_config(g)
+    for key in ("architecture", "family", "hidden", "intermediate", "layers", "heads", "kvHeads", "headDim", "vocab",
+                "rotaryDim", "window", "period", "slidingWindow", "rope", "qkNorm", "ffnGate", "activation", "maxContext"):
+        assert got["config"][key] == getattr(c, key), key
+    for key in ("epsilon", "theta", "localTheta", "attentionScale", "ropeScale"):
+        assert got["config"][key] == pytest.approx(getattr(c, key), rel=1e-12), key
+    assert got["config"]["bias"] == c.bias
+    assert got["dataOffset"] == g.dataOffset
+    assert {t[0]: t[1:] for t in got["tensors"]} == {n: [t.type, t.offset, t.bytes] for n, t in g.tensors.items()}
+
+
+@needs_node
+def test_node_rejects_a_non_gguf_file(tmp_path):
+    p = tmp_path / "x.bin"
+    p.write_bytes(b"\0" * 64)
+    r = subprocess.run([NODE, RUNNER, str(p), "config"], capture_output=True, text=True, timeout=60)
+    assert r.returncode != 0 and "Select a GGUF model file." in r.stderr
+
+
+@pytest.mark.gpu
+@needs_node
+def test_node_engine_tiny_greedy_matches_oracle(tiny_file):
+    from oracle import orc
+    from webgpu_amd.context import attention_memory
+    path, f = tiny_file
+    g = parse_gguf_header(f, f.size)
+    c = model_config(g)
+    ids = synth.prompt_ids(c.vocab, 8)
+    got = run_node(path, "greedy", ",".join(map(str, ids)), 4, timeout=300)
+    ora = orc.OracleModel(f, g, c, 512, attention_memory(c, 512, 128)["capacities"])
+    try:
+        want = ora.forward(ids, 0)
+        expected, _ = ora.greedy(ids, 4)
+    finally:
+        ora.close()
+    logits = np.asarray(got["logits"], np.float64)
+    err = float(np.abs(logits - want).max() / np.abs(want).max())
+    assert err <= 1e-3, err
+    assert got["tokens"] == list(expected)

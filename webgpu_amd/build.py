@@ -50,7 +50,30 @@ def build(jobs: int = 6) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
+    build_napi()
     return OUT
+
+
+NODE_INCLUDE = os.environ.get("NODE_INCLUDE", "/usr/include/node")
+NAPI_SRC = os.path.join(HERE, "node", "wgd_napi.cc")
+NAPI_OUT = os.path.join(HERE, "node", "wgd_napi.node")
+
+
+def build_napi() -> str:
+    """The Node addon over libwgd's C ABI (g++, no node-gyp): N-API symbols resolve against
+    the node binary at load time, libwgd.so through an $ORIGIN rpath. Skipped when the Node
+    headers are absent."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        return ""
+    tmp = NAPI_OUT + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-DNODE_GYP_MODULE_NAME=wgd_napi",
+           "-I" + NODE_INCLUDE, "-I" + os.path.join(HERE, "..", "include"), NAPI_SRC,
+           "-L" + HERE, "-lwgd", "-Wl,-rpath,$ORIGIN/..", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"N-API addon build failed:\n{r.stderr}")
+    os.replace(tmp, NAPI_OUT)
+    return NAPI_OUT
 
 
 if __name__ == "__main__":

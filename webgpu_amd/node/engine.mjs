@@ -1,0 +1,170 @@
+// engine.mjs — PagedEngine for the Node host (src/core/engine.ts:26-324) over the libwgd
+// N-API addon: load(path, options) -> ModelInfo, async generate(prompt ids, options) ->
+// TokenEvents, forward, reset, dispose, info and the greedy sample. GGUF parsing,
+// modelConfig and ring sizing run here as in gguf.ts / context.ts; weights are uploaded
+// once and stay resident (the weight pager collapses), and every forward and greedy decode
+// step runs in libwgd on the GPU. Tokenizers are outside this runtime: prompts are ids, or
+// any object with chat(messages) -> ids, decode(ids) -> string and eos passed as tokenizer.
+import { createRequire } from 'module';
+import { readGGUF, modelConfig, FileSource } from './gguf.mjs';
+import { attentionMemory, validateContext, outputLimit, MAX_CONTEXT } from './context.mjs';
+
+const require = createRequire(import.meta.url);
+const addon = require('./wgd_napi.node');
+
+const BATCHES = [1, 8, 16, 32, 64, 128];
+
+/** The wgd_model_config fields for a ModelConfig (field names of include/wgd.h). */
+export function configStruct(c, context, batch, tied) {
+  const gemma = c.family === 'gemma3';
+  return {
+    family: gemma ? 1 : 0, rope_adjacent: c.rope === 'norm' ? 1 : 0,
+    hidden: c.hidden, intermediate: c.intermediate, layers: c.layers, heads: c.heads, kv_heads: c.kvHeads,
+    head_dim: c.headDim, vocab: c.vocab, rotary_dim: c.rotaryDim, window: gemma ? c.window : c.slidingWindow,
+    period: c.period, qk_norm: c.qkNorm ? 1 : 0, ffn_gate: c.ffnGate ? 1 : 0, gelu: c.activation === 'gelu' ? 1 : 0,
+    bias_q: c.bias.q ? 1 : 0, bias_k: c.bias.k ? 1 : 0, bias_v: c.bias.v ? 1 : 0, bias_output: c.bias.output ? 1 : 0,
+    tied_output: tied ? 1 : 0, context, batch,
+    epsilon: c.epsilon, theta: c.theta, local_theta: c.localTheta, attention_scale: c.attentionScale,
+    rope_scale: c.ropeScale, embed_scale: c.architecture === 'gemma3' ? Math.sqrt(c.hidden) : 1,
+  };
+}
+
+export class PagedEngine {
+  constructor(progress) {
+    this.progress = progress || (() => {});
+    this.ctx = null; this.model = null; this.source = null; this.gguf = null; this.config = null;
+    this.context = 512; this.batch = 128; this.kvCapacities = [];
+    this.busy = false; this.disposed = false; this.tokensInCache = [];
+  }
+
+  /** PagedEngine.load (engine.ts:51-114): parse, configure, upload, seal. */
+  load(path, options = {}) {
+    const o = Object.assign({ contextLength: 512, batchSize: 128, gpuBudgetMiB: null, device: 0 }, options);
+    this.context = o.contextLength; this.batch = o.batchSize;
+    validateContext(this.context);
+    if (!BATCHES.includes(this.batch)) throw new Error('Batch size must be 1, 8, 16, 32, 64 or 128.');
+    if (o.gpuBudgetMiB !== null && (!Number.isInteger(o.gpuBudgetMiB) || o.gpuBudgetMiB < 512))
+      throw new Error('GPU budget must be at least 512 MiB.');
+    this.source = new FileSource(path);
+    this.progress({ phase: 'loading', detail: 'Reading GGUF metadata', fraction: 0.05 });
+    this.gguf = readGGUF(this.source);
+    const c = this.config = modelConfig(this.gguf);
+    validateContext(this.context, c.maxContext);
+    this.kvCapacities = attentionMemory(c, this.context, this.batch).capacities;
+    this.ctx = addon.create(o.device, o.gpuBudgetMiB);
+    try {
+      const tied = !this.gguf.tensors.has('output.weight');
+      this.model = addon.modelCreate(this.ctx, configStruct(c, this.context, this.batch, tied), Int32Array.from(this.kvCapacities));
+      const tensors = [...this.gguf.tensors.values()].filter((t) => (t.dims.length === 1 || t.dims.length === 2) &&
+        (!t.name.startsWith('blk.') || Number(t.name.split('.')[1]) < c.layers));
+      tensors.forEach((t, i) => {
+        addon.modelTensor(this.model, t.name, t.type, t.dims, this.source.read(t.offset, t.bytes));
+        if (i % 64 === 0) this.progress({ phase: 'loading', detail: 'Uploading weights', fraction: 0.1 + (0.85 * i) / tensors.length });
+      });
+      addon.modelReady(this.model);
+      this.progress({ phase: 'ready', detail: 'Ready.', fraction: 1 });
+      return this.info();
+    } catch (e) {
+      this.dispose();
+      throw e;
+    }
+  }
+
+  info() {
+    return { config: this.config, fileBytes: this.source ? this.source.size : 0, adapter: this.ctx ? addon.adapterName(this.ctx) : '',
+      contextLength: this.context, batchSize: this.batch, stats: this.stats() };
+  }
+
+  stats() {
+    if (!this.ctx) return { gpuBytes: 0, peakGpuBytes: 0 };
+    const m = addon.memory(this.ctx);
+    return { gpuBytes: m.allocated, peakGpuBytes: m.peak };
+  }
+
+  /** forward(ids, start, logits) (engine.ts:138-180): the last row's logits, or null. */
+  forward(ids, start, logits) {
+    if (!this.model) throw new Error('Load a model first.');
+    const out = logits ? new Float32Array(this.config.vocab) : null;
+    addon.modelForward(this.model, Int32Array.from(ids), start, out);
+    return out;
+  }
+
+  /** forward + sample(T=0) with the argmax taken on the device. */
+  forwardArgmax(ids, start) {
+    if (!this.model) throw new Error('Load a model first.');
+    return addon.modelForward(this.model, Int32Array.from(ids), start, null);
+  }
+
+  /** `count` greedy steps on the device from `token` at position `start`. */
+  decode(token, start, count) {
+    return Array.from(addon.modelDecode(this.model, token, start, count));
+  }
+
+  /** PagedEngine.generate (engine.ts:257-301), greedy: prefix reuse, output limit, chunked
+   * prefill and the busy guard; the decode loop runs on the device `chunk` tokens at a time. */
+  async *generate(prompt, options = {}, tokenizer = null, chunk = 32) {
+    if (this.busy) throw new Error('A generation is already running.');
+    if (this.disposed || !this.model) throw new Error('Load a model first.');
+    const o = Object.assign({ maxTokens: 128, temperature: 0 }, options);
+    if (!Number.isInteger(o.maxTokens) || o.maxTokens < 1 || o.maxTokens > MAX_CONTEXT) throw new Error(`maxTokens must be 1–${MAX_CONTEXT}.`);
+    if (o.temperature !== 0) throw new Error('Only greedy decoding (temperature 0) is implemented by this runtime.');
+    const ids = tokenizer ? Array.from(tokenizer.chat(prompt)) : Array.from(prompt, Number);
+    if (!ids.length) throw new Error('Provide a non-empty prompt.');
+    const eos = new Set((tokenizer && tokenizer.eos) || []);
+    this.busy = true;
+    try {
+      const limit = outputLimit(o.maxTokens, ids.length, this.context);
+      let shared = 0;
+      while (shared < ids.length && shared < this.tokensInCache.length && ids[shared] === this.tokensInCache[shared]) shared++;
+      shared = Math.min(shared, ids.length - 1);
+      if (shared < this.tokensInCache.length && this.kvCapacities.some((cap) => cap < this.context)) shared = 0;
+      const started = Date.now();
+      this.tokensInCache = this.tokensInCache.slice(0, shared);
+      let token = -1;
+      for (let i = shared; i < ids.length; i += this.batch) {
+        const part = ids.slice(i, i + this.batch);
+        if (i + part.length === ids.length) token = this.forwardArgmax(part, i);
+        else this.forward(part, i, false);
+        this.tokensInCache.push(...part);
+      }
+      const generated = [];
+      let text = '';
+      let pending = [];
+      for (let i = 0; i < limit; i++) {
+        if (i > 0) {
+          if (!pending.length) pending = this.decode(token, this.tokensInCache.length, Math.min(chunk, limit - i));
+          this.tokensInCache.push(token);
+          token = pending.shift();
+        }
+        if (eos.has(token)) break;
+        generated.push(token);
+        const full = tokenizer ? tokenizer.decode(generated) : '';
+        const delta = full.slice(text.length);
+        text = full;
+        yield { token, text, delta, tokens: generated.length, promptTokens: ids.length, contextLength: this.context,
+          seconds: (Date.now() - started) / 1000, stats: this.stats() };
+      }
+    } catch (e) {
+      this.tokensInCache = [];
+      throw e;
+    } finally {
+      this.busy = false;
+    }
+  }
+
+  reset() {
+    if (this.busy) throw new Error('Stop generation first.');
+    this.tokensInCache = [];
+  }
+
+  dispose() {
+    this.disposed = true;
+    if (this.model) addon.modelDestroy(this.model);
+    this.model = null;
+    if (this.ctx) addon.destroy(this.ctx);
+    this.ctx = null;
+    if (this.source) this.source.close();
+    this.source = null;
+    this.tokensInCache = [];
+  }
+}
