@@ -185,6 +185,28 @@ def test_attention_long_context_and_ring(gpu, context, start, batch, window, cap
         gpu.destroy(b)
 
 
+# Prompt batches (the matrix-core path for head_dim 64/128/256): causal from position 0,
+# a batch deep in the context, a ragged batch with one query head per KV head, a sliding
+# window shorter than the batch's key range, and a wrapped ring.
+@pytest.mark.parametrize("heads,kvh,hd,start,batch,window,capacity", [
+    (32, 8, 128, 0, 128, 4096, 1024), (32, 8, 128, 384, 128, 4096, 1024), (8, 8, 64, 100, 37, 4096, 256),
+    (16, 2, 256, 50, 20, 24, 128), (8, 2, 128, 1000, 48, 200, 256), (6, 2, 64, 7, 131, 4096, 512)])
+def test_prompt_attention_batches(gpu, heads, kvh, hd, start, batch, window, capacity):
+    rng = np.random.default_rng(start + batch)
+    q = rng.standard_normal(batch * heads * hd).astype(np.float32) * 2
+    k = rng.standard_normal(capacity * kvh * hd).astype(np.float32)
+    v = rng.standard_normal(capacity * kvh * hd).astype(np.float32)
+    bufs = [gpu.upload(a, nm) for a, nm in ((q, "q"), (k, "k"), (v, "v"))] + [gpu.buffer(q.nbytes, "y")]
+    scale = 1 / np.sqrt(hd)
+    gpu.attention(*bufs, heads, kvh, hd, start, scale, window, capacity, capacity, batch)
+    got = gpu.read_f32(bufs[3], q.size)
+    want = orc.attention(q, k, v, heads, kvh, hd, start, scale, window, capacity, batch)
+    err = np.abs(got - want).max()
+    assert np.all(np.isfinite(got)) and err <= 1e-4, f"max abs error {err:.3e}"
+    for b in bufs:
+        gpu.destroy(b)
+
+
 # ---------------------------------------------------------------- verify.ts:55-66, verify-qwen.ts:87-97
 def test_norm_and_qk_norm_rope(gpu):
     heads, hd, start, n = 4, 8, 3, 2

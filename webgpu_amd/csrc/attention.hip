@@ -164,6 +164,182 @@ __global__ __launch_bounds__(128) void k_attention_combine(const float *part, fl
   }
 }
 
+// Prompt batches on the f32 matrix cores (v_mfma_f32_16x16x4_f32: f32 products, f32 sums, as
+// the f32 shader computes them). A wavefront owns 16 consecutive queries of one head; the
+// four wavefronts of a workgroup share one kv head and stage 64-key tiles of K (row-major)
+// and V (transposed) in LDS. Scores are formed transposed, S^T = K Q^T, so lane (g, c) holds
+// keys 4g..4g+3 of query row c: a row's running max and sum live in its own lanes (two
+// cross-lane steps per tile) and the probabilities already sit in the B-operand layout of
+// O^T += V^T P^T. The k summation index of both products walks d (and keys) in the order
+// 16t + 4g + u, which turns each operand fetch into one 16-byte LDS read per four MFMAs.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t AP_T = 64;  // keys per LDS tile
+
+template <uint32_t HD>
+constexpr size_t attn_prompt_lds() { return sizeof(float) * ((size_t)AP_T * (HD + 4) + (size_t)HD * (AP_T + 4)); }
+
+template <uint32_t HD>
+__global__ __launch_bounds__(256) void k_attn_prompt(AttnK a) {
+  constexpr uint32_t T = AP_T, KS = HD + 4, VS = T + 4, NT = HD / 16;
+  extern __shared__ float lds[];
+  float *Ks = lds, *Vt = lds + T * KS;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, c = lane & 15;
+  const uint32_t kv = blockIdx.x, z = blockIdx.z, group = a.group;
+  const uint32_t nqt = (a.batch + 15) / 16;
+  const uint32_t ti = blockIdx.y * 4 + wv, qt = ti / group, h = kv * group + ti % group;
+  const bool tile_ok = qt < nqt;
+  const uint32_t s0 = a.start_dev ? (uint32_t)*a.start_dev : a.start;
+
+  // Key range of the workgroup (its first and last query tiles), split into z chunks.
+  const uint32_t qt_lo = blockIdx.y * 4 / group;
+  const uint32_t qt_hi = min((blockIdx.y * 4 + 3) / group, nqt - 1);
+  const uint32_t first_end = s0 + qt_lo * 16 + 1, last_end = s0 + min(a.batch, (qt_hi + 1) * 16);
+  const uint32_t begin0 = first_end - min(first_end, a.window);
+  uint32_t chunk = (last_end - begin0 + a.nsplit - 1) / a.nsplit;
+  chunk = (chunk + T - 1) / T * T;
+  const uint32_t lo = begin0 + z * chunk, hi = min(lo + chunk, last_end);
+
+  // This lane's query row and the keys it sees; the wavefront's union of them.
+  const uint32_t b = qt * 16 + c;
+  const bool row_ok = tile_ok && b < a.batch;
+  const uint32_t end_b = s0 + b + 1, begin_b = end_b - min(end_b, a.window);
+  const uint32_t wq_end = s0 + (tile_ok ? min(a.batch, qt * 16 + 16) : 0);
+  const uint32_t wq_first = s0 + qt * 16 + 1, wq_begin = wq_first - min(wq_first, a.window);
+
+  f32x4 qr[NT], o[NT];
+#pragma unroll
+  for (uint32_t t = 0; t < NT; t++) {
+    qr[t] = row_ok ? *(const f32x4 *)(a.q + ((uint64_t)b * a.heads + h) * HD + 16 * t + 4 * g) : f32x4{0, 0, 0, 0};
+    o[t] = f32x4{0, 0, 0, 0};
+  }
+  float m = -INFINITY, l = 0.f;
+
+  for (uint32_t t0 = lo; t0 < hi; t0 += T) {
+    __syncthreads();
+    for (uint32_t i = tid; i < T * HD / 4; i += 256) {
+      const uint32_t j = i / (HD / 4), d = (i % (HD / 4)) * 4, t = t0 + j;
+      f32x4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+      if (t < hi) {
+        const uint64_t src = ((uint64_t)(t % a.capacity) * a.kvh + kv) * HD + d;
+        kk = *(const f32x4 *)(a.k + src);
+        vv = *(const f32x4 *)(a.v + src);
+      }
+      *(f32x4 *)(Ks + j * KS + d) = kk;
+      Vt[(d + 0) * VS + j] = vv.x;
+      Vt[(d + 1) * VS + j] = vv.y;
+      Vt[(d + 2) * VS + j] = vv.z;
+      Vt[(d + 3) * VS + j] = vv.w;
+    }
+    __syncthreads();
+    const uint32_t k0 = max(t0, wq_begin), k1 = min(min(t0 + T, hi), wq_end);
+    if (!tile_ok || k0 >= k1) continue;  // wavefront-uniform: none of its rows sees this tile
+    float s[4][4];
+    bool live[4];
+#pragma unroll
+    for (uint32_t kb = 0; kb < 4; kb++) {
+      const uint32_t kt = t0 + kb * 16;
+      live[kb] = kt < k1 && kt + 16 > k0;
+      f32x4 acc = {0, 0, 0, 0};
+      if (live[kb]) {
+#pragma unroll
+        for (uint32_t t = 0; t < NT; t++) {
+          const f32x4 kf = *(const f32x4 *)(Ks + (kb * 16 + c) * KS + 16 * t + 4 * g);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qr[t].x, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qr[t].y, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qr[t].z, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qr[t].w, acc, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < 4; r++) {
+        const uint32_t key = kt + 4 * g + r;
+        s[kb][r] = (live[kb] && row_ok && key >= begin_b && key < end_b && key < hi) ? acc[r] * a.scale : -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (uint32_t r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float corr = mn == -INFINITY ? 1.f : expf(m - mn);
+    float sum = 0.f;
+#pragma unroll
+    for (uint32_t kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (uint32_t r = 0; r < 4; r++) {
+        const float p = s[kb][r] == -INFINITY ? 0.f : expf(s[kb][r] - mn);
+        s[kb][r] = p;
+        sum += p;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    l = l * corr + sum;
+    m = mn;
+#pragma unroll
+    for (uint32_t t = 0; t < NT; t++) o[t] *= corr;
+#pragma unroll
+    for (uint32_t kb = 0; kb < 4; kb++) {
+      if (!live[kb]) continue;
+#pragma unroll
+      for (uint32_t t = 0; t < NT; t++) {
+        const f32x4 vf = *(const f32x4 *)(Vt + (t * 16 + c) * VS + kb * 16 + 4 * g);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, s[kb][0], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, s[kb][1], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, s[kb][2], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, s[kb][3], o[t], 0, 0, 0);
+      }
+    }
+  }
+  if (!row_ok) return;
+  // lane (g, c) holds O^T[16t + 4g + r][row c]
+  const uint64_t row = (uint64_t)b * a.heads + h;
+  if (a.nsplit == 1) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (uint32_t t = 0; t < NT; t++) *(f32x4 *)(a.y + row * HD + 16 * t + 4 * g) = o[t] * inv;
+  } else {
+    float *pp = a.part + ((uint64_t)z * a.batch * a.heads + row) * (HD + 2);
+    if (g == 0) { pp[0] = m; pp[1] = l; }
+#pragma unroll
+    for (uint32_t t = 0; t < NT; t++)
+#pragma unroll
+      for (uint32_t r = 0; r < 4; r++) pp[2 + 16 * t + 4 * g + r] = o[t][r];
+  }
+}
+
+template <uint32_t HD>
+static hipError_t launch_attn_prompt(hipStream_t s, AttnK a, const AttnArgs &in, uint32_t keys) {
+  const uint32_t nqt = (in.batch + 15) / 16;
+  const uint32_t wgs = in.kv_heads * ((nqt * a.group + 3) / 4);
+  const uint32_t tiles = (keys + AP_T - 1) / AP_T;
+  const uint32_t want = ((uint32_t)device_cu_count() + wgs - 1) / wgs;
+  uint32_t nsplit = tiles < want ? tiles : want;
+  if (nsplit < 1) nsplit = 1;
+  if (nsplit > 1) {
+    const uint64_t per_split = (uint64_t)in.batch * in.heads * (in.hd + 2);
+    const uint64_t fit = in.partial ? in.partial_floats / per_split : 0;
+    if (fit < nsplit) nsplit = fit > 1 ? (uint32_t)fit : 1;
+  }
+  a.nsplit = nsplit;
+  constexpr size_t lds = attn_prompt_lds<HD>();
+  static bool big_lds = false;
+  if (lds > 65536 && !big_lds) {
+    WGD_HIP(hipFuncSetAttribute((const void *)k_attn_prompt<HD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    big_lds = true;
+  }
+  hipLaunchKernelGGL(k_attn_prompt<HD>, dim3(in.kv_heads, (nqt * a.group + 3) / 4, nsplit), dim3(256), lds, s, a);
+  WGD_HIP(hipGetLastError());
+  if (nsplit > 1) {
+    hipLaunchKernelGGL(k_attention_combine, dim3(in.batch * in.heads), dim3(128), 0, s, (const float *)in.partial,
+                       in.y, in.batch * in.heads, in.hd, nsplit);
+    WGD_HIP(hipGetLastError());
+  }
+  return hipSuccess;
+}
+
 static uint32_t tile_keys(uint32_t hd) {
   uint32_t t = 4096 / hd;
   if (t > 64) t = 64;
@@ -184,12 +360,6 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
   a.heads = in.heads; a.kvh = in.kv_heads; a.hd = in.hd; a.start = in.start; a.start_dev = in.start_dev;
   a.scale = in.scale; a.window = in.window; a.capacity = in.capacity; a.batch = in.batch;
   a.group = in.heads / in.kv_heads;
-  a.qb = a.group >= 16 ? 1 : 16 / a.group;
-  if (a.qb > in.batch) a.qb = in.batch;
-  a.R = a.qb * a.group;
-  if (a.R > 16) return hipErrorInvalidValue;
-  a.T = tile_keys(in.hd);
-  const uint32_t qblocks = (in.batch + a.qb - 1) / a.qb;
   // Key range bound: the host start when known, else the whole ring/window.
   uint32_t keys = in.window;
   if (!in.start_dev) {
@@ -200,6 +370,16 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
   } else if (keys > in.capacity + in.batch) {
     keys = in.capacity + in.batch;
   }
+  const bool aligned = ((uintptr_t)in.q | (uintptr_t)in.k | (uintptr_t)in.v | (uintptr_t)in.y) % 16 == 0;
+  if (aligned && in.hd == 64) return launch_attn_prompt<64>(s, a, in, keys);
+  if (aligned && in.hd == 128) return launch_attn_prompt<128>(s, a, in, keys);
+  if (aligned && in.hd == 256) return launch_attn_prompt<256>(s, a, in, keys);
+  a.qb = a.group >= 16 ? 1 : 16 / a.group;
+  if (a.qb > in.batch) a.qb = in.batch;
+  a.R = a.qb * a.group;
+  if (a.R > 16) return hipErrorInvalidValue;
+  a.T = tile_keys(in.hd);
+  const uint32_t qblocks = (in.batch + a.qb - 1) / a.qb;
   uint32_t tiles = (keys + a.T - 1) / a.T;
   uint32_t want = (uint32_t)device_cu_count() * 4 / (in.kv_heads * qblocks);
   uint32_t nsplit = tiles < want ? tiles : want;

@@ -308,15 +308,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
   const QRsrc rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int)a.wbytes, 0x00020000);
   // this thread's staging item: weight row-tile / column / row, and activation token / half
   const uint32_t wrt = tid >> 5, wcc = (tid >> 4) & 1, wr = tid & 15;
-  const uint32_t xt = tid >> 1, xhf = tid & 1;
-  const bool xlive = n0 + xt < a.batch;
-  const float *xrow = a.x + (uint64_t)(n0 + xt + a.input_offset) * a.cols;
+  // activations: tokens xt + 16 i, columns 4 xc..4 xc+3 of the tile (a wavefront reads four
+  // whole 256-byte token rows per load)
+  const uint32_t xt = tid >> 4, xc = tid & 15;
+  const float *xrow = a.x + (uint64_t)(n0 + xt + a.input_offset) * a.cols + 4 * xc;
   QWeights<TYPE> wreg;
   float4 xr[8];
   auto fetch = [&](uint32_t k0) {
     wreg.fetch(a, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc);
 #pragma unroll
-    for (int i = 0; i < 8; i++) xr[i] = xlive ? *(const float4 *)(xrow + k0 + 32 * xhf + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 8; i++)
+      xr[i] = n0 + xt + 16 * i < a.batch ? *(const float4 *)(xrow + (uint64_t)16 * i * a.cols + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
   };
   auto stage = [&](uint32_t k0) {
     float v[32];
@@ -334,12 +336,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
     for (int i = 0; i < 8; i++) {
       split2(xr[i].x, xr[i].y, h[2 * i], l[2 * i]);
       split2(xr[i].z, xr[i].w, h[2 * i + 1], l[2 * i + 1]);
-    }
-    uint16_t *eh = xh + xt * QG_P + 32 * xhf, *el = xl + xt * QG_P + 32 * xhf;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      *(uint4 *)(eh + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
-      *(uint4 *)(el + 8 * i) = make_uint4(l[4 * i], l[4 * i + 1], l[4 * i + 2], l[4 * i + 3]);
+      const uint32_t o = (xt + 16 * i) * QG_P + 4 * xc;
+      *(uint2 *)(xh + o) = make_uint2(h[2 * i], h[2 * i + 1]);
+      *(uint2 *)(xl + o) = make_uint2(l[2 * i], l[2 * i + 1]);
     }
   };
   f32x4 acc[4][4];
@@ -367,28 +366,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[i], Bh[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[i], Bl[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al[i], Bh[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[j], Ah[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bl[j], Ah[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[j], Al[i], acc[i][j], 0, 0, 0);
         }
     }
     __syncthreads();
   }
-  // D layout: lane holds rows 4 * (lane / 16) + e, token lane % 16 of each 16 x 16 tile
+  // The products are formed as X W^T, so lane (g, c) of tile (i, j) holds tokens 16 j + 4 g + e
+  // of row 16 i + c: each store writes 16 consecutive rows of four tokens.
+  const uint32_t row0 = m0 + wm * 64 + (lane & 15);
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t tok = n0 + wn * 64 + 16 * j + (lane & 15);
-    if (tok >= a.batch) continue;
+  for (int j = 0; j < 4; j++)
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int e = 0; e < 4; e++) {
+      const uint32_t tok = n0 + wn * 64 + 16 * j + 4 * (lane >> 4) + e;
+      if (tok >= a.batch) continue;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint32_t row = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+      for (int i = 0; i < 4; i++) {
+        const uint32_t row = row0 + 16 * i;
         if (row >= a.rows) continue;
         if (a.part) a.part[((uint64_t)z * a.batch + tok) * a.rows + row] = acc[i][j][e];
         else a.y[(uint64_t)tok * a.stride + a.row_base + row] = acc[i][j][e];
       }
-  }
+    }
 }
 
 // y[tok * stride + row_base + row] = sum over splits z (in order) of part[z][tok][row].
