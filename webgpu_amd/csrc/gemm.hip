@@ -185,15 +185,28 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 // The prompt GEMM of the planar layouts (Q4_K, Q6_K, Q8_0; the decode matvec's weights). A
 // workgroup owns QG_M = 128 weight rows x QG_N = 128 tokens and a K span (split-K when the
 // rows alone give too few workgroups; partial sums are added in split order by
-// k_gemm_reduce, so results do not depend on timing). Per 64-column K tile, every weight
-// of the workgroup's rows is dequantized once, from coalesced 16-byte planar loads (one
-// 32-element chunk of one row per thread), split into bf16 hi + lo and stored in LDS; the
-// activation tile is split the same way. Four wavefronts each compute 64 rows x 64 tokens,
-// sixteen 16 x 16 accumulators, three MFMAs per product (hi*hi + hi*lo + lo*hi). The next
-// K tile's loads are issued before the MFMAs of the current one; 74 KB of LDS lets two
-// workgroups share a CU, so one's dequantization overlaps the other's MFMAs.
-constexpr uint32_t QG_M = 128, QG_N = 128, QG_K = 64, QG_P = QG_K + 8;  // LDS row pitch (bf16)
-constexpr uint32_t QG_LDS = 4 * QG_M * QG_P * 2;  // w hi, w lo, x hi, x lo
+// k_gemm_reduce, so results do not depend on timing). The activations are split into bf16
+// (hi, lo) once per input by k_gemm_split, already in MFMA fragment order, so a
+// workgroup's activation tile is a plain 32 KB copy. Per 64-column K tile every weight of
+// the workgroup's rows is dequantized once, from coalesced 16-byte planar loads (one
+// 32-element chunk of one row per thread), split the same way and stored in fragment
+// order. Four wavefronts each compute 64 rows x 64 tokens, sixteen 16 x 16 accumulators,
+// three MFMAs per product (hi*hi + hi*lo + lo*hi). The next K tile's loads are issued
+// before the MFMAs of the current one; 64 KB of LDS lets two workgroups share a CU, so
+// one's dequantization overlaps the other's MFMAs.
+//
+// Fragment order of a 128 x 64 operand tile (rows of weights, or tokens):
+// [hl][b][s][g][c][e] holds element (16 b + c, 32 s + 8 g + e) of the hi (hl = 0) or lo
+// part. Lane 16 g + c of an MFMA takes the 16 bytes at fragment (hl, b, s) + 16 * lane, so
+// every operand fetch is one conflict-free 1 KB LDS read.
+constexpr uint32_t QG_M = 128, QG_N = 128, QG_K = 64;
+constexpr uint32_t QG_FRAG = 512;                 // bf16 of one 16 x 32 fragment
+constexpr uint32_t QG_TILE = 2 * 8 * 2 * QG_FRAG;  // bf16 of a 128 x 64 tile, hi and lo
+constexpr uint32_t QG_LDS = 2 * QG_TILE * 2;       // bytes: weight tile + activation tile
+
+__host__ __device__ constexpr uint32_t frag_at(uint32_t hl, uint32_t b, uint32_t s, uint32_t g, uint32_t c) {
+  return ((((hl * 8 + b) * 2 + s) * 4 + g) * 16 + c) * 8;
+}
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -209,9 +222,33 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
 struct QGemm {
   const uint8_t *w; uint32_t wbytes;
   uint32_t C, bpr, nbp;  // chunk columns, blocks per row, blocks of the padded matrix
-  const float *x; float *y; float *part;
-  uint32_t cols, rows, stride, row_base, input_offset, batch, kspan;
+  const uint16_t *xs; float *y; float *part;
+  uint32_t cols, rows, stride, row_base, batch, kspan;
 };
+
+// Activations [batch][cols] f32 -> fragment-ordered bf16 (hi, lo) tiles, tile (n, k) at
+// (n * cols / 64 + k) * QG_TILE; tokens past the batch up to the tile are zero. One thread
+// per eight consecutive columns of a token.
+__global__ __launch_bounds__(256) void k_gemm_split(const float *x, uint16_t *xs, uint32_t cols, uint32_t batch,
+                                                    uint32_t count) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const uint32_t c8 = cols / 8, tok = i / c8, k = (i % c8) * 8;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+  if (tok < batch) {
+    a = *(const float4 *)(x + (uint64_t)tok * cols + k);
+    b = *(const float4 *)(x + (uint64_t)tok * cols + k + 4);
+  }
+  uint32_t h[4], l[4];
+  split2(a.x, a.y, h[0], l[0]);
+  split2(a.z, a.w, h[1], l[1]);
+  split2(b.x, b.y, h[2], l[2]);
+  split2(b.z, b.w, h[3], l[3]);
+  const uint32_t r = tok % QG_N, kk = k % QG_K;
+  uint16_t *t = xs + ((uint64_t)(tok / QG_N) * (cols / QG_K) + k / QG_K) * QG_TILE;
+  *(uint4 *)(t + frag_at(0, r / 16, kk / 32, (kk % 32) / 8, r % 16)) = make_uint4(h[0], h[1], h[2], h[3]);
+  *(uint4 *)(t + frag_at(1, r / 16, kk / 32, (kk % 32) / 8, r % 16)) = make_uint4(l[0], l[1], l[2], l[3]);
+}
 
 typedef __amdgpu_buffer_rsrc_t QRsrc;
 __device__ __forceinline__ uint4 qld16(QRsrc r, uint32_t off) {
@@ -301,24 +338,23 @@ template <> struct QWeights<Q8_0> {
 template <int TYPE>
 __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t qlds[];
-  uint16_t *wh = qlds, *wl = qlds + QG_M * QG_P, *xh = qlds + 2 * QG_M * QG_P, *xl = qlds + 3 * QG_M * QG_P;
+  uint16_t *wt = qlds, *xt = qlds + QG_TILE;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv & 1, wn = wv >> 1;
   const uint32_t m0 = blockIdx.x * QG_M, n0 = blockIdx.y * QG_N, z = blockIdx.z;
   const uint32_t kb = z * a.kspan, ke = kb + a.kspan < a.cols ? kb + a.kspan : a.cols;
   const QRsrc rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int)a.wbytes, 0x00020000);
-  // this thread's staging item: weight row-tile / column / row, and activation token / half
+  // this thread's weights: row tile wrt, 32-column half wcc of the K tile, row wr
   const uint32_t wrt = tid >> 5, wcc = (tid >> 4) & 1, wr = tid & 15;
-  // activations: tokens xt + 16 i, columns 4 xc..4 xc+3 of the tile (a wavefront reads four
-  // whole 256-byte token rows per load)
-  const uint32_t xt = tid >> 4, xc = tid & 15;
-  const float *xrow = a.x + (uint64_t)(n0 + xt + a.input_offset) * a.cols + 4 * xc;
+  // this thread's activation copy: 16-byte chunks tid + 256 i of the tile
+  const uint16_t *xsrc = a.xs + (uint64_t)blockIdx.y * (a.cols / QG_K) * QG_TILE + 8 * tid;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   QWeights<TYPE> wreg;
-  float4 xr[8];
+  u32x4 xr[8];
   auto fetch = [&](uint32_t k0) {
     wreg.fetch(a, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc);
+    const uint16_t *src = xsrc + (uint64_t)(k0 / QG_K) * QG_TILE;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      xr[i] = n0 + xt + 16 * i < a.batch ? *(const float4 *)(xrow + (uint64_t)16 * i * a.cols + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 8; i++) xr[i] = *(const u32x4 *)(src + 2048 * i);
   };
   auto stage = [&](uint32_t k0) {
     float v[32];
@@ -326,41 +362,33 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
     uint32_t h[16], l[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) split2(v[2 * i], v[2 * i + 1], h[i], l[i]);
-    uint16_t *dh = wh + (wrt * 16 + wr) * QG_P + 32 * wcc, *dl = wl + (wrt * 16 + wr) * QG_P + 32 * wcc;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      *(uint4 *)(dh + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
-      *(uint4 *)(dl + 8 * i) = make_uint4(l[4 * i], l[4 * i + 1], l[4 * i + 2], l[4 * i + 3]);
+    for (uint32_t g = 0; g < 4; g++) {
+      *(uint4 *)(wt + frag_at(0, wrt, wcc, g, wr)) = make_uint4(h[4 * g], h[4 * g + 1], h[4 * g + 2], h[4 * g + 3]);
+      *(uint4 *)(wt + frag_at(1, wrt, wcc, g, wr)) = make_uint4(l[4 * g], l[4 * g + 1], l[4 * g + 2], l[4 * g + 3]);
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      split2(xr[i].x, xr[i].y, h[2 * i], l[2 * i]);
-      split2(xr[i].z, xr[i].w, h[2 * i + 1], l[2 * i + 1]);
-      const uint32_t o = (xt + 16 * i) * QG_P + 4 * xc;
-      *(uint2 *)(xh + o) = make_uint2(h[2 * i], h[2 * i + 1]);
-      *(uint2 *)(xl + o) = make_uint2(l[2 * i], l[2 * i + 1]);
-    }
+    for (int i = 0; i < 8; i++) *(u32x4 *)(xt + 8 * tid + 2048 * i) = xr[i];
   };
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint32_t ar = wm * 64 + (lane & 15), br = wn * 64 + (lane & 15), kq = 8 * (lane >> 4);
   fetch(kb);
   for (uint32_t k0 = kb; k0 < ke; k0 += QG_K) {
     stage(k0);
     __syncthreads();
     if (k0 + QG_K < ke) fetch(k0 + QG_K);  // next tile's loads fly during the MFMAs
 #pragma unroll
-    for (uint32_t ks = 0; ks < QG_K; ks += 32) {
+    for (uint32_t ks = 0; ks < 2; ks++) {
       bf16x8 Ah[4], Al[4], Bh[4], Bl[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        Ah[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(wh + (ar + 16 * i) * QG_P + ks + kq));
-        Al[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(wl + (ar + 16 * i) * QG_P + ks + kq));
-        Bh[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(xh + (br + 16 * i) * QG_P + ks + kq));
-        Bl[i] = __builtin_bit_cast(bf16x8, *(const uint4 *)(xl + (br + 16 * i) * QG_P + ks + kq));
+      for (uint32_t i = 0; i < 4; i++) {
+        Ah[i] = *(const bf16x8 *)(wt + frag_at(0, wm * 4 + i, ks, 0, 0) + 8 * lane);
+        Al[i] = *(const bf16x8 *)(wt + frag_at(1, wm * 4 + i, ks, 0, 0) + 8 * lane);
+        Bh[i] = *(const bf16x8 *)(xt + frag_at(0, wn * 4 + i, ks, 0, 0) + 8 * lane);
+        Bl[i] = *(const bf16x8 *)(xt + frag_at(1, wn * 4 + i, ks, 0, 0) + 8 * lane);
       }
 #pragma unroll
       for (int i = 0; i < 4; i++)
@@ -410,18 +438,18 @@ static bool qgemm_supported(const Matrix &w) {
   return w.type == Q8_0 && w.cols % QG_K == 0;
 }
 
-// K span per workgroup: enough splits for a workgroup per CU, each at least 512 columns
-// (whole 256-column blocks; 64 for Q8_0), and no more partial sums than the scratch holds.
+// K span per workgroup: enough splits for two workgroups per CU (64 KB of LDS each), each
+// at least one 256-column block (64 columns for Q8_0), and no more partial sums than the
+// scratch holds.
 static uint32_t qgemm_kspan(const Matrix &w, uint32_t batch, uint64_t scratch_floats) {
   const uint32_t align = w.type == Q8_0 ? QG_K : 256;
   const uint32_t tiles = ((w.rows + QG_M - 1) / QG_M) * ((batch + QG_N - 1) / QG_N);
-  const uint32_t target = (uint32_t)device_cu_count();
-  uint32_t splits = tiles >= target ? 1 : (target + tiles - 1) / tiles;
-  if (splits > w.cols / 512) splits = w.cols / 512 > 0 ? w.cols / 512 : 1;
+  const uint32_t target = 2 * (uint32_t)device_cu_count();
+  uint32_t splits = tiles >= target ? 1 : target / tiles;
   const uint32_t units = w.cols / align;
   if (splits > units) splits = units;
-  while (splits > 1 && (uint64_t)splits * batch * w.rows > scratch_floats) splits--;
   if (splits > 16) splits = 16;
+  while (splits > 1 && (uint64_t)splits * batch * w.rows > scratch_floats) splits--;
   const uint32_t per = (units + splits - 1) / splits;
   return per * align;
 }
@@ -433,20 +461,32 @@ uint64_t gemm_split_floats(const Matrix &w, uint32_t batch) {
   return splits > 1 ? (uint64_t)splits * batch * w.rows : 0;
 }
 
+uint64_t gemm_input_elems(uint32_t cols, uint32_t batch) {
+  return (uint64_t)(batch + QG_N - 1) / QG_N * QG_N * cols * 2;
+}
+
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                uint32_t row_base, uint32_t input_offset, uint32_t batch, const GemmScratch &scratch) {
+                uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch) {
   if (!w.rows || !batch) return hipSuccess;
-  if (qgemm_supported(w)) {
+  const float *xb = x + (uint64_t)input_offset * w.cols;
+  if (qgemm_supported(w) && scratch && scratch->xs && scratch->xs_elems >= gemm_input_elems(w.cols, batch) &&
+      (uintptr_t)xb % 16 == 0) {
     const uint64_t wbytes = planar_bytes(w.type, w.cols, w.rows);
     if (wbytes >= (1ull << 31)) return hipErrorInvalidValue;
+    if (scratch->xs_of != xb || scratch->xs_cols != w.cols || scratch->xs_batch != batch) {
+      const uint32_t count = (uint32_t)(gemm_input_elems(w.cols, batch) / 16);
+      hipLaunchKernelGGL(k_gemm_split, dim3((count + 255) / 256), dim3(256), 0, s, xb, scratch->xs, w.cols, batch, count);
+      WGD_HIP(hipGetLastError());
+      scratch->xs_of = xb; scratch->xs_cols = w.cols; scratch->xs_batch = batch;
+    }
     QGemm q;
     q.w = w.data; q.wbytes = (uint32_t)wbytes;
     q.C = w.cols / chunk_elems(w.type); q.bpr = w.cols / block_size(w.type); q.nbp = q.bpr * (uint32_t)tile_rows(w.rows);
-    q.x = x; q.y = y; q.cols = w.cols; q.rows = w.rows; q.stride = stride; q.row_base = row_base;
-    q.input_offset = input_offset; q.batch = batch;
-    q.kspan = qgemm_kspan(w, batch, scratch.p ? scratch.floats : 0);
+    q.xs = scratch->xs; q.y = y; q.cols = w.cols; q.rows = w.rows; q.stride = stride; q.row_base = row_base;
+    q.batch = batch;
+    q.kspan = qgemm_kspan(w, batch, scratch->p ? scratch->floats : 0);
     const uint32_t splits = (w.cols + q.kspan - 1) / q.kspan;
-    q.part = splits > 1 ? scratch.p : nullptr;
+    q.part = splits > 1 ? scratch->p : nullptr;
     const dim3 grid((w.rows + QG_M - 1) / QG_M, (batch + QG_N - 1) / QG_N, splits);
     auto go = [&](auto kernel) {
       static bool big = false;  // opt in above the default dynamic LDS limit once per kernel

@@ -65,18 +65,27 @@ hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *d
 
 // ---------------------------------------------------------------- launchers
 
-// Scratch for the prompt GEMM's split-K partial sums; gemm_split_floats() is what a launch
-// of w over `batch` tokens can use (0: it does not split). Less scratch means fewer splits.
-struct GemmScratch { float *p = nullptr; uint64_t floats = 0; };
+// Scratch of the prompt GEMM on planar weights. p: split-K partial sums, of which
+// gemm_split_floats() is what a launch of w over `batch` tokens can use (0: it does not
+// split; less scratch means fewer splits). xs: the activations split into bf16 (hi, lo) in
+// MFMA fragment order, gemm_input_elems() of them (without it the generic kernel runs).
+// xs_of/xs_cols/xs_batch name the activations xs holds, so GEMMs over the same input split
+// it once; whoever rewrites that memory clears xs_of.
+struct GemmScratch {
+  float *p = nullptr; uint64_t floats = 0;
+  uint16_t *xs = nullptr; uint64_t xs_elems = 0;
+  const float *xs_of = nullptr; uint32_t xs_cols = 0, xs_batch = 0;
+};
 uint64_t gemm_split_floats(const Matrix &w, uint32_t batch);
+uint64_t gemm_input_elems(uint32_t cols, uint32_t batch);
 // y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]: the
 // generic kernel for small batches of GGUF-layout weights, else the MFMA dequant-GEMM.
 hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                  uint32_t row_base, uint32_t input_offset, uint32_t batch, const GemmScratch &scratch = GemmScratch());
+                  uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch = nullptr);
 hipError_t matmul_generic(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
                           uint32_t row_base, uint32_t input_offset, uint32_t batch);
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                uint32_t row_base, uint32_t input_offset, uint32_t batch, const GemmScratch &scratch = GemmScratch());
+                uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch = nullptr);
 
 hipError_t dequant(hipStream_t s, int type, const uint8_t *w, float *out, uint64_t count);
 hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *ids, float *out,

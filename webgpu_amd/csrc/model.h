@@ -25,6 +25,8 @@ struct wgd_context {
   uint64_t mv_qx_bytes = 0;
   float *gemm_part = nullptr;         // split-K partial sums of wgd_matmul's prompt GEMM
   uint64_t gemm_part_floats = 0;
+  uint16_t *gemm_xs = nullptr;        // its input split into bf16 (hi, lo)
+  uint64_t gemm_xs_elems = 0;
 };
 
 namespace wgd {

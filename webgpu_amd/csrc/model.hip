@@ -163,31 +163,38 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
   const uint32_t H = c.hidden, qd = c.heads * c.head_dim, kd = c.kv_heads * c.head_dim, F = c.intermediate;
+  // The GEMMs of one input (q, k, v; gate, up) share its bf16 split: xs_of is cleared
+  // whenever the input buffer is rewritten.
+  GemmScratch gs = m->gemm_part;
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
     WGD_HIP(norm(s, m->hidden, L.attn_norm, m->normed, H, c.epsilon, n));
-    WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, m->gemm_part));
+    gs.xs_of = nullptr;
+    WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->q, L.bq, n, qd));
-    WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, m->gemm_part));
+    WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->k, L.bk, n, kd));
-    WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, n, m->gemm_part));
+    WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->v, L.bv, n, kd));
     WGD_HIP(attention_block(m, l, n, start, start_dev));
-    WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, n, m->gemm_part));
+    gs.xs_of = nullptr;
+    WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->proj, L.bo, n, H));
     if (is_gemma(m)) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, n));
     else WGD_HIP(add(s, m->proj, m->hidden, n * H));
     WGD_HIP(norm(s, m->hidden, L.ffn_norm, m->normed, H, c.epsilon, n));
-    WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, n, m->gemm_part));
+    gs.xs_of = nullptr;
+    WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, n, &gs));
     float *ffn_in = m->up;
     if (c.ffn_gate) {
-      WGD_HIP(matmul(s, L.gate, m->normed, m->gate, F, 0, 0, n, m->gemm_part));
+      WGD_HIP(matmul(s, L.gate, m->normed, m->gate, F, 0, 0, n, &gs));
       WGD_HIP(glu(s, m->gate, m->up, m->prod, n * F, c.gelu));
       ffn_in = m->prod;
     } else {
       WGD_HIP(activate(s, m->up, n * F));
     }
-    WGD_HIP(matmul(s, L.down, ffn_in, m->down, H, 0, 0, n, m->gemm_part));
+    gs.xs_of = nullptr;
+    WGD_HIP(matmul(s, L.down, ffn_in, m->down, H, 0, 0, n, &gs));
     if (is_gemma(m)) WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, n));
     else WGD_HIP(add(s, m->down, m->hidden, n * H));
   }
@@ -573,15 +580,24 @@ int wgd_model_ready(wgd_model *m) {
       }
   }
   if (rc) return rc;
-  // split-K scratch of the prompt GEMMs: the most any layer matrix uses at the batch size
-  uint64_t gp = 0;
+  // prompt GEMM scratch: split-K sums and the bf16 split input, the most any layer matrix
+  // uses at the batch size
+  uint64_t gp = 0, gx = 0;
   for (const Layer &L : m->L)
     for (const Matrix *w : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
-      if (w->data) gp = std::max(gp, gemm_split_floats(*w, (uint32_t)c.batch));
+      if (w->data) {
+        gp = std::max(gp, gemm_split_floats(*w, (uint32_t)c.batch));
+        gx = std::max(gx, gemm_input_elems(w->cols, (uint32_t)c.batch));
+      }
   if (gp && !m->gemm_part.p) {
     rc = alloc_t(m, gp, "prompt GEMM split sums", &m->gemm_part.p);
     if (rc) return rc;
     m->gemm_part.floats = gp;
+  }
+  if (gx && !m->gemm_part.xs) {
+    rc = alloc_t(m, gx, "prompt GEMM split input", &m->gemm_part.xs);
+    if (rc) return rc;
+    m->gemm_part.xs_elems = gx;
   }
   // The quantized decode path needs every matrix in a type the integer matvec reads.
   const Matrix &head_w = m->have_output && !c.tied_output ? m->output : m->embd;

@@ -291,9 +291,20 @@ int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
     if (rc) return rc;
     ctx->gemm_part = (float *)p; ctx->gemm_part_floats = gp;
   }
+  // and the bf16 split of the input, re-made on every call
+  const uint64_t gx = gemm_input_elems(cols, batch);
+  if (m.layout == LAYOUT_PLANAR && gx > ctx->gemm_xs_elems) {
+    ctx_free(ctx, ctx->gemm_xs);
+    ctx->gemm_xs = nullptr; ctx->gemm_xs_elems = 0;
+    void *p = nullptr;
+    int rc = ctx_alloc(ctx, gx * 2, "GEMM split input", &p);
+    if (rc) return rc;
+    ctx->gemm_xs = (uint16_t *)p; ctx->gemm_xs_elems = gx;
+  }
   GemmScratch gs;
   gs.p = ctx->gemm_part; gs.floats = ctx->gemm_part_floats;
-  return ctx_check(ctx, matmul(ctx->stream, m, (const float *)x->ptr, (float *)y->ptr, stride, row_base, input_offset, batch, gs), "matmul");
+  gs.xs = ctx->gemm_xs; gs.xs_elems = ctx->gemm_xs_elems;
+  return ctx_check(ctx, matmul(ctx->stream, m, (const float *)x->ptr, (float *)y->ptr, stride, row_base, input_offset, batch, &gs), "matmul");
 }
 
 uint64_t wgd_quantized_bytes(uint32_t cols) { return qx_bytes(cols); }
