@@ -14,6 +14,7 @@
 // 64 per LDS tile.
 #include "internal.h"
 #include "decode.h"
+#include "split.h"
 
 namespace wgd {
 
@@ -195,40 +196,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 // before the MFMAs of the current one; 64 KB of LDS lets two workgroups share a CU, so
 // one's dequantization overlaps the other's MFMAs.
 //
-// Fragment order of a 128 x 64 operand tile (rows of weights, or tokens):
-// [hl][b][s][g][c][e] holds element (16 b + c, 32 s + 8 g + e) of the hi (hl = 0) or lo
-// part. Lane 16 g + c of an MFMA takes the 16 bytes at fragment (hl, b, s) + 16 * lane, so
-// every operand fetch is one conflict-free 1 KB LDS read.
-constexpr uint32_t QG_M = 128, QG_N = 128, QG_K = 64;
-constexpr uint32_t QG_FRAG = 512;                 // bf16 of one 16 x 32 fragment
-constexpr uint32_t QG_TILE = 2 * 8 * 2 * QG_FRAG;  // bf16 of a 128 x 64 tile, hi and lo
-constexpr uint32_t QG_LDS = 2 * QG_TILE * 2;       // bytes: weight tile + activation tile
-
-__host__ __device__ constexpr uint32_t frag_at(uint32_t hl, uint32_t b, uint32_t s, uint32_t g, uint32_t c) {
-  return ((((hl * 8 + b) * 2 + s) * 4 + g) * 16 + c) * 8;
-}
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two floats -> (hi, lo) bf16 pairs with hi = RN(v), lo = RN(v - hi) (native gfx950 packing).
-__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-  const f32x2 v = {a, b};
-  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-  const f32x2 back = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
-  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - back, bf16x2));
-}
+// The weight tile is kept in LDS in the activations' fragment order (split.h), as rows.
+constexpr uint32_t QG_M = 128, QG_N = SPLIT_N, QG_K = SPLIT_K, QG_TILE = SPLIT_TILE;
+constexpr uint32_t QG_LDS = 2 * QG_TILE * 2;  // bytes: weight tile + activation tile
 
 struct QGemm {
   const uint8_t *w; uint32_t wbytes;
   uint32_t C, bpr, nbp;  // chunk columns, blocks per row, blocks of the padded matrix
   const uint16_t *xs; float *y; float *part;
-  uint32_t cols, rows, stride, row_base, batch, kspan;
+  uint32_t cols, rows, stride, row_base, batch, kspan, accumulate;
 };
 
-// Activations [batch][cols] f32 -> fragment-ordered bf16 (hi, lo) tiles, tile (n, k) at
-// (n * cols / 64 + k) * QG_TILE; tokens past the batch up to the tile are zero. One thread
-// per eight consecutive columns of a token.
+// Activations [batch][cols] f32 -> the split form (split.h); tokens past the batch up to the
+// tile are zero. One thread per eight consecutive columns of a token.
 __global__ __launch_bounds__(256) void k_gemm_split(const float *x, uint16_t *xs, uint32_t cols, uint32_t batch,
                                                     uint32_t count) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
@@ -239,15 +219,7 @@ __global__ __launch_bounds__(256) void k_gemm_split(const float *x, uint16_t *xs
     a = *(const float4 *)(x + (uint64_t)tok * cols + k);
     b = *(const float4 *)(x + (uint64_t)tok * cols + k + 4);
   }
-  uint32_t h[4], l[4];
-  split2(a.x, a.y, h[0], l[0]);
-  split2(a.z, a.w, h[1], l[1]);
-  split2(b.x, b.y, h[2], l[2]);
-  split2(b.z, b.w, h[3], l[3]);
-  const uint32_t r = tok % QG_N, kk = k % QG_K;
-  uint16_t *t = xs + ((uint64_t)(tok / QG_N) * (cols / QG_K) + k / QG_K) * QG_TILE;
-  *(uint4 *)(t + frag_at(0, r / 16, kk / 32, (kk % 32) / 8, r % 16)) = make_uint4(h[0], h[1], h[2], h[3]);
-  *(uint4 *)(t + frag_at(1, r / 16, kk / 32, (kk % 32) / 8, r % 16)) = make_uint4(l[0], l[1], l[2], l[3]);
+  split_store8(xs, cols, tok, k, a, b);
 }
 
 typedef __amdgpu_buffer_rsrc_t QRsrc;
@@ -414,21 +386,28 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
       for (int i = 0; i < 4; i++) {
         const uint32_t row = row0 + 16 * i;
         if (row >= a.rows) continue;
-        if (a.part) a.part[((uint64_t)z * a.batch + tok) * a.rows + row] = acc[i][j][e];
-        else a.y[(uint64_t)tok * a.stride + a.row_base + row] = acc[i][j][e];
+        if (a.part) {
+          a.part[((uint64_t)z * a.batch + tok) * a.rows + row] = acc[i][j][e];
+        } else {
+          float *py = a.y + (uint64_t)tok * a.stride + a.row_base + row;
+          *py = a.accumulate ? *py + acc[i][j][e] : acc[i][j][e];
+        }
       }
     }
 }
 
-// y[tok * stride + row_base + row] = sum over splits z (in order) of part[z][tok][row].
+// y[tok * stride + row_base + row] = sum over splits z (in order) of part[z][tok][row]
+// (accumulate: y plus that sum).
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float *part, float *y, uint32_t rows, uint32_t batch,
-                                                     uint32_t splits, uint32_t stride, uint32_t row_base) {
+                                                     uint32_t splits, uint32_t stride, uint32_t row_base,
+                                                     uint32_t accumulate) {
   const uint64_t n = (uint64_t)rows * batch;
   for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
     float v = 0.f;
     for (uint32_t z = 0; z < splits; z++) v += part[(uint64_t)z * n + i];
     const uint32_t tok = (uint32_t)(i / rows), row = (uint32_t)(i % rows);
-    y[(uint64_t)tok * stride + row_base + row] = v;
+    float *py = y + (uint64_t)tok * stride + row_base + row;
+    *py = accumulate ? *py + v : v;
   }
 }
 
@@ -465,12 +444,15 @@ uint64_t gemm_input_elems(uint32_t cols, uint32_t batch) {
   return (uint64_t)(batch + QG_N - 1) / QG_N * QG_N * cols * 2;
 }
 
+bool gemm_splits_input(const Matrix &w, const GemmScratch *scratch, uint32_t batch) {
+  return qgemm_supported(w) && scratch && scratch->xs && scratch->xs_elems >= gemm_input_elems(w.cols, batch);
+}
+
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch) {
+                uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch, bool accumulate) {
   if (!w.rows || !batch) return hipSuccess;
   const float *xb = x + (uint64_t)input_offset * w.cols;
-  if (qgemm_supported(w) && scratch && scratch->xs && scratch->xs_elems >= gemm_input_elems(w.cols, batch) &&
-      (uintptr_t)xb % 16 == 0) {
+  if (gemm_splits_input(w, scratch, batch) && (uintptr_t)xb % 16 == 0) {
     const uint64_t wbytes = planar_bytes(w.type, w.cols, w.rows);
     if (wbytes >= (1ull << 31)) return hipErrorInvalidValue;
     if (scratch->xs_of != xb || scratch->xs_cols != w.cols || scratch->xs_batch != batch) {
@@ -483,7 +465,7 @@ hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32
     q.w = w.data; q.wbytes = (uint32_t)wbytes;
     q.C = w.cols / chunk_elems(w.type); q.bpr = w.cols / block_size(w.type); q.nbp = q.bpr * (uint32_t)tile_rows(w.rows);
     q.xs = scratch->xs; q.y = y; q.cols = w.cols; q.rows = w.rows; q.stride = stride; q.row_base = row_base;
-    q.batch = batch;
+    q.batch = batch; q.accumulate = accumulate ? 1u : 0u;
     q.kspan = qgemm_kspan(w, batch, scratch->p ? scratch->floats : 0);
     const uint32_t splits = (w.cols + q.kspan - 1) / q.kspan;
     q.part = splits > 1 ? scratch->p : nullptr;
@@ -502,10 +484,11 @@ hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32
       uint32_t blocks = (uint32_t)((n + 255) / 256);
       if (blocks > 4096) blocks = 4096;
       hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(256), 0, s, (const float *)q.part, y, w.rows, batch, splits,
-                         stride, row_base);
+                         stride, row_base, q.accumulate);
     }
     return hipGetLastError();
   }
+  if (accumulate) return hipErrorInvalidValue;  // only the planar-weight GEMM adds into y
   if (w.cols % KT) return hipErrorInvalidValue;
   GemmArgs a;
   a.w = w.data; a.type = w.type; a.layout = w.layout;

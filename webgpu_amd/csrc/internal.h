@@ -78,20 +78,29 @@ struct GemmScratch {
 };
 uint64_t gemm_split_floats(const Matrix &w, uint32_t batch);
 uint64_t gemm_input_elems(uint32_t cols, uint32_t batch);
+// True when a GEMM of w over `batch` tokens runs the planar-weight kernel on the split input
+// (and may add into y).
+bool gemm_splits_input(const Matrix &w, const GemmScratch *scratch, uint32_t batch);
 // y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]: the
 // generic kernel for small batches of GGUF-layout weights, else the MFMA dequant-GEMM.
+// accumulate (planar weights with split-input scratch only): y[...] += the sum.
 hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                  uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch = nullptr);
+                  uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch = nullptr,
+                  bool accumulate = false);
 hipError_t matmul_generic(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
                           uint32_t row_base, uint32_t input_offset, uint32_t batch);
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch = nullptr);
+                uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch = nullptr,
+                bool accumulate = false);
 
 hipError_t dequant(hipStream_t s, int type, const uint8_t *w, float *out, uint64_t count);
 hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *ids, float *out,
                  uint32_t hidden, uint32_t n, double scale);
 hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_t n, float eps,
                 uint32_t batch);
+// norm() that also writes its output in the prompt GEMM's split form into xs (n % 64 == 0).
+hipError_t norm_split(hipStream_t s, const float *x, const float *w, float *y, uint16_t *xs, uint32_t n, float eps,
+                      uint32_t batch);
 // mode 0: Q/K norm + half-split, 1: half-split, 2: adjacent pairs. start_dev overrides start.
 hipError_t rope(hipStream_t s, float *x, const float *w, uint32_t heads, uint32_t hd,
                 uint32_t start, const int32_t *start_dev, float theta, float scale, float eps,
@@ -106,6 +115,9 @@ hipError_t attention(hipStream_t s, const AttnArgs &a);
 uint64_t attention_scratch_floats(uint32_t heads, uint32_t hd, uint32_t batch, uint32_t max_keys);
 hipError_t add(hipStream_t s, const float *delta, float *state, uint32_t n);
 hipError_t glu(hipStream_t s, const float *gate, const float *up, float *y, uint32_t n, int act);
+// glu() over [batch][cols] that also writes y in the prompt GEMM's split form (cols % 64 == 0).
+hipError_t glu_split(hipStream_t s, const float *gate, const float *up, float *y, uint16_t *xs, uint32_t cols,
+                     uint32_t batch, int act);
 hipError_t bias_add(hipStream_t s, float *y, const float *b, uint32_t n, uint32_t width);
 hipError_t activate(hipStream_t s, float *x, uint32_t n);
 // argmax over finite values, first index wins; writes -1 when none is finite.

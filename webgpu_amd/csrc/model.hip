@@ -163,13 +163,23 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
   const uint32_t H = c.hidden, qd = c.heads * c.head_dim, kd = c.kv_heads * c.head_dim, F = c.intermediate;
-  // The GEMMs of one input (q, k, v; gate, up) share its bf16 split: xs_of is cleared
-  // whenever the input buffer is rewritten.
+  // The GEMMs of one input (q, k, v; gate, up) share its bf16 split (xs_of names the buffer
+  // it was made from and is cleared whenever that buffer is rewritten). RMSNorm and the GLU
+  // write the split themselves when the GEMM after them runs on it; the O and down GEMMs
+  // then add straight into the residual stream.
   GemmScratch gs = m->gemm_part;
+  auto norm_for = [&](const float *w, const Matrix &first) -> hipError_t {
+    if (!gemm_splits_input(first, &gs, n)) {
+      gs.xs_of = nullptr;
+      return norm(s, m->hidden, w, m->normed, H, c.epsilon, n);
+    }
+    gs.xs_of = m->normed; gs.xs_cols = H; gs.xs_batch = n;
+    return norm_split(s, m->hidden, w, m->normed, gs.xs, H, c.epsilon, n);
+  };
+  const bool gemma = is_gemma(m);
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
-    WGD_HIP(norm(s, m->hidden, L.attn_norm, m->normed, H, c.epsilon, n));
-    gs.xs_of = nullptr;
+    WGD_HIP(norm_for(L.attn_norm, L.q));
     WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->q, L.bq, n, qd));
     WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, &gs));
@@ -178,25 +188,38 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
     WGD_HIP(bias(s, m->v, L.bv, n, kd));
     WGD_HIP(attention_block(m, l, n, start, start_dev));
     gs.xs_of = nullptr;
-    WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, n, &gs));
-    WGD_HIP(bias(s, m->proj, L.bo, n, H));
-    if (is_gemma(m)) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, n));
-    else WGD_HIP(add(s, m->proj, m->hidden, n * H));
-    WGD_HIP(norm(s, m->hidden, L.ffn_norm, m->normed, H, c.epsilon, n));
-    gs.xs_of = nullptr;
+    if (!gemma && !L.bo && gemm_splits_input(L.o, &gs, n)) {
+      WGD_HIP(matmul(s, L.o, m->att, m->hidden, H, 0, 0, n, &gs, true));
+    } else {
+      WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, n, &gs));
+      WGD_HIP(bias(s, m->proj, L.bo, n, H));
+      if (gemma) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, n));
+      else WGD_HIP(add(s, m->proj, m->hidden, n * H));
+    }
+    WGD_HIP(norm_for(L.ffn_norm, L.up));
     WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, n, &gs));
     float *ffn_in = m->up;
     if (c.ffn_gate) {
       WGD_HIP(matmul(s, L.gate, m->normed, m->gate, F, 0, 0, n, &gs));
-      WGD_HIP(glu(s, m->gate, m->up, m->prod, n * F, c.gelu));
+      if (gemm_splits_input(L.down, &gs, n)) {
+        WGD_HIP(glu_split(s, m->gate, m->up, m->prod, gs.xs, F, n, c.gelu));
+        gs.xs_of = m->prod; gs.xs_cols = F; gs.xs_batch = n;
+      } else {
+        WGD_HIP(glu(s, m->gate, m->up, m->prod, n * F, c.gelu));
+        gs.xs_of = nullptr;
+      }
       ffn_in = m->prod;
     } else {
       WGD_HIP(activate(s, m->up, n * F));
+      gs.xs_of = nullptr;
     }
-    gs.xs_of = nullptr;
-    WGD_HIP(matmul(s, L.down, ffn_in, m->down, H, 0, 0, n, &gs));
-    if (is_gemma(m)) WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, n));
-    else WGD_HIP(add(s, m->down, m->hidden, n * H));
+    if (!gemma && gemm_splits_input(L.down, &gs, n)) {
+      WGD_HIP(matmul(s, L.down, ffn_in, m->hidden, H, 0, 0, n, &gs, true));
+    } else {
+      WGD_HIP(matmul(s, L.down, ffn_in, m->down, H, 0, 0, n, &gs));
+      if (gemma) WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, n));
+      else WGD_HIP(add(s, m->down, m->hidden, n * H));
+    }
   }
   return hipSuccess;
 }

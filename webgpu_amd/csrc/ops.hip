@@ -9,6 +9,7 @@
 // (pos * scale * theta^(-2i/rot)) with f64 sin/cos so long positions track the f64 oracle.
 #include "internal.h"
 #include "decode.h"
+#include "split.h"
 
 namespace wgd {
 
@@ -37,6 +38,40 @@ __global__ __launch_bounds__(256) void k_norm(const float *x, const float *w, fl
 hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_t n, float eps, uint32_t batch) {
   if (!batch || !n) return hipSuccess;
   hipLaunchKernelGGL(k_norm, dim3(batch), dim3(256), 0, s, x, w, y, n, eps);
+  return hipGetLastError();
+}
+
+// One token per workgroup, eight consecutive elements per thread step: the f32 output and
+// its split form for the GEMMs that read it.
+__global__ __launch_bounds__(256) void k_norm_split(const float *x, const float *w, float *y, uint16_t *xs,
+                                                    uint32_t n, float eps) {
+  __shared__ float red[4];
+  const uint32_t tok = blockIdx.x;
+  const float *xr = x + (uint64_t)tok * n;
+  float *yr = y + (uint64_t)tok * n;
+  float s = 0.f;
+  for (uint32_t k = 8 * threadIdx.x; k < n; k += 8 * 256) {
+    const float4 a = *(const float4 *)(xr + k), b = *(const float4 *)(xr + k + 4);
+    s += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+  }
+  s = block_sum_256(s, red);
+  const float inv = 1.f / sqrtf(s / (float)n + eps);
+  for (uint32_t k = 8 * threadIdx.x; k < n; k += 8 * 256) {
+    float4 a = *(const float4 *)(xr + k), b = *(const float4 *)(xr + k + 4);
+    const float4 wa = *(const float4 *)(w + k), wb = *(const float4 *)(w + k + 4);
+    a = make_float4(a.x * inv * wa.x, a.y * inv * wa.y, a.z * inv * wa.z, a.w * inv * wa.w);
+    b = make_float4(b.x * inv * wb.x, b.y * inv * wb.y, b.z * inv * wb.z, b.w * inv * wb.w);
+    *(float4 *)(yr + k) = a;
+    *(float4 *)(yr + k + 4) = b;
+    split_store8(xs, n, tok, k, a, b);
+  }
+}
+
+hipError_t norm_split(hipStream_t s, const float *x, const float *w, float *y, uint16_t *xs, uint32_t n, float eps,
+                      uint32_t batch) {
+  if (!batch) return hipSuccess;
+  if (n % SPLIT_K || ((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) % 16) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_norm_split, dim3(batch), dim3(256), 0, s, x, w, y, xs, n, eps);
   return hipGetLastError();
 }
 
@@ -136,6 +171,39 @@ hipError_t add(hipStream_t s, const float *delta, float *state, uint32_t n) {
 hipError_t glu(hipStream_t s, const float *gate, const float *up, float *y, uint32_t n, int act) {
   if (!n) return hipSuccess;
   hipLaunchKernelGGL(k_glu, grid_for(n), dim3(256), 0, s, gate, up, y, n, act);
+  return hipGetLastError();
+}
+
+// Eight consecutive elements of one token per thread.
+__global__ __launch_bounds__(256) void k_glu_split(const float *g, const float *u, float *y, uint16_t *xs,
+                                                   uint32_t cols, uint32_t count, int act) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const uint32_t c8 = cols / 8, tok = i / c8, k = (i % c8) * 8;
+  const uint64_t o = (uint64_t)tok * cols + k;
+  float v[8];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const float4 gv = *(const float4 *)(g + o + 4 * h), uv = *(const float4 *)(u + o + 4 * h);
+    const float gg[4] = {gv.x, gv.y, gv.z, gv.w}, uu[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float x = gg[e];
+      v[4 * h + e] = (act ? gelu_tanh_f(x) : x / (1.f + expf(-x))) * uu[e];
+    }
+  }
+  const float4 a = make_float4(v[0], v[1], v[2], v[3]), b = make_float4(v[4], v[5], v[6], v[7]);
+  *(float4 *)(y + o) = a;
+  *(float4 *)(y + o + 4) = b;
+  split_store8(xs, cols, tok, k, a, b);
+}
+
+hipError_t glu_split(hipStream_t s, const float *gate, const float *up, float *y, uint16_t *xs, uint32_t cols,
+                     uint32_t batch, int act) {
+  if (!batch) return hipSuccess;
+  if (cols % SPLIT_K || ((uintptr_t)gate | (uintptr_t)up | (uintptr_t)y) % 16) return hipErrorInvalidValue;
+  const uint32_t count = batch * (cols / 8);
+  hipLaunchKernelGGL(k_glu_split, dim3((count + 255) / 256), dim3(256), 0, s, gate, up, y, xs, cols, count, act);
   return hipGetLastError();
 }
 hipError_t bias_add(hipStream_t s, float *y, const float *b, uint32_t n, uint32_t width) {

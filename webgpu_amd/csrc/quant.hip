@@ -273,10 +273,11 @@ int device_cu_count() {
 }
 
 hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
-                  uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch) {
+                  uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch, bool accumulate) {
   if (!w.rows || !batch) return hipSuccess;
   if ((batch > 4 || w.layout != LAYOUT_GGUF) && w.cols % 64 == 0)
-    return gemm(s, w, x, y, stride, row_base, input_offset, batch, scratch);
+    return gemm(s, w, x, y, stride, row_base, input_offset, batch, scratch, accumulate);
+  if (accumulate) return hipErrorInvalidValue;
   return matmul_generic(s, w, x, y, stride, row_base, input_offset, batch);
 }
 
