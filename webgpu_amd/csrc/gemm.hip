@@ -200,11 +200,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 constexpr uint32_t QG_M = 128, QG_N = SPLIT_N, QG_K = SPLIT_K, QG_TILE = SPLIT_TILE;
 constexpr uint32_t QG_LDS = 2 * QG_TILE * 2;  // bytes: weight tile + activation tile
 
-struct QGemm {
+// One weight matrix of a grouped launch: its planar geometry, the row-tile count, and where
+// its rows go (y, or rows [row0, row0 + rows) of the group's split-K partial sums).
+struct QJob {
   const uint8_t *w; uint32_t wbytes;
   uint32_t C, bpr, nbp;  // chunk columns, blocks per row, blocks of the padded matrix
-  const uint16_t *xs; float *y; float *part;
-  uint32_t cols, rows, stride, row_base, batch, kspan, accumulate;
+  uint32_t rows, tiles, kind, row0;
+  float *y; uint32_t stride, row_base;
+};
+constexpr uint32_t QG_MAX_JOBS = 3;
+// Matrices that read the same activations, launched together: workgroups (tile, split)
+// over the concatenated row tiles; kind 0 / 1 selects the launch's first / second type.
+struct QGemm {
+  QJob job[QG_MAX_JOBS]; uint32_t njobs;
+  const uint16_t *xs; float *part;
+  uint32_t cols, batch, kspan, rows_total, accumulate;
 };
 
 // Activations [batch][cols] f32 -> the split form (split.h); tokens past the batch up to the
@@ -234,7 +244,7 @@ __device__ __forceinline__ uint4 qld16(QRsrc r, uint32_t off) {
 template <int TYPE> struct QWeights;
 template <> struct QWeights<Q4_K> {
   uint4 q, h;
-  __device__ void fetch(const QGemm &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+  __device__ void fetch(const QJob &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
     q = qld16(rw, ((T * a.C + c) * 16 + r) * 16);
     h = qld16(rw, a.nbp * 128 + ((T * a.bpr + c / 8) * 16 + r) * 16);
   }
@@ -259,7 +269,7 @@ template <> struct QWeights<Q4_K> {
 };
 template <> struct QWeights<Q6_K> {
   uint4 q; uint2 qh; uint32_t sc, d;
-  __device__ void fetch(const QGemm &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+  __device__ void fetch(const QJob &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
     const uint32_t tc = (T * a.C + c) * 16 + r;
     q = qld16(rw, tc * 16);
     typedef unsigned int u2 __attribute__((ext_vector_type(2)));
@@ -289,7 +299,7 @@ template <> struct QWeights<Q6_K> {
 template <> struct QWeights<Q8_0> {
   uint4 q[2]; uint32_t d[2];
   // chunks 2c and 2c + 1 (16 elements each, one Q8_0 block): c counts 32-element columns
-  __device__ void fetch(const QGemm &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+  __device__ void fetch(const QJob &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
 #pragma unroll
     for (int u = 0; u < 2; u++) q[u] = qld16(rw, ((T * a.C + 2 * c + u) * 16 + r) * 16);
     d[0] = d[1] = __builtin_amdgcn_raw_buffer_load_b16(rw, a.nbp * 32 + ((T * a.bpr + c) * 16 + r) * 2, 0, 0);
@@ -308,13 +318,12 @@ template <> struct QWeights<Q8_0> {
 };
 
 template <int TYPE>
-__global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t qlds[];
+__device__ __forceinline__ void gemm_tile(const QGemm &a, const QJob &jb, uint32_t mt, uint16_t *qlds) {
   uint16_t *wt = qlds, *xt = qlds + QG_TILE;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv & 1, wn = wv >> 1;
-  const uint32_t m0 = blockIdx.x * QG_M, n0 = blockIdx.y * QG_N, z = blockIdx.z;
+  const uint32_t m0 = mt * QG_M, n0 = blockIdx.y * QG_N, z = blockIdx.z;
   const uint32_t kb = z * a.kspan, ke = kb + a.kspan < a.cols ? kb + a.kspan : a.cols;
-  const QRsrc rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int)a.wbytes, 0x00020000);
+  const QRsrc rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(jb.w), 0, (int)jb.wbytes, 0x00020000);
   // this thread's weights: row tile wrt, 32-column half wcc of the K tile, row wr
   const uint32_t wrt = tid >> 5, wcc = (tid >> 4) & 1, wr = tid & 15;
   // this thread's activation copy: 16-byte chunks tid + 256 i of the tile
@@ -323,7 +332,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
   QWeights<TYPE> wreg;
   u32x4 xr[8];
   auto fetch = [&](uint32_t k0) {
-    wreg.fetch(a, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc);
+    wreg.fetch(jb, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc);
     const uint16_t *src = xsrc + (uint64_t)(k0 / QG_K) * QG_TILE;
 #pragma unroll
     for (int i = 0; i < 8; i++) xr[i] = *(const u32x4 *)(src + 2048 * i);
@@ -385,30 +394,69 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const uint32_t row = row0 + 16 * i;
-        if (row >= a.rows) continue;
+        if (row >= jb.rows) continue;
         if (a.part) {
-          a.part[((uint64_t)z * a.batch + tok) * a.rows + row] = acc[i][j][e];
+          a.part[((uint64_t)z * a.batch + tok) * a.rows_total + jb.row0 + row] = acc[i][j][e];
         } else {
-          float *py = a.y + (uint64_t)tok * a.stride + a.row_base + row;
+          float *py = jb.y + (uint64_t)tok * jb.stride + jb.row_base + row;
           *py = a.accumulate ? *py + acc[i][j][e] : acc[i][j][e];
         }
       }
     }
 }
 
-// y[tok * stride + row_base + row] = sum over splits z (in order) of part[z][tok][row]
-// (accumulate: y plus that sum).
-__global__ __launch_bounds__(256) void k_gemm_reduce(const float *part, float *y, uint32_t rows, uint32_t batch,
-                                                     uint32_t splits, uint32_t stride, uint32_t row_base,
-                                                     uint32_t accumulate) {
-  const uint64_t n = (uint64_t)rows * batch;
+// blockIdx.x walks the jobs' row tiles in order; a job of kind 1 runs the second type.
+template <int T0, int T1>
+__global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t qlds[];
+  uint32_t t = blockIdx.x, j = 0;
+  while (j + 1 < a.njobs && t >= a.job[j].tiles) { t -= a.job[j].tiles; j++; }
+  const QJob &jb = a.job[j];
+  if (T0 == T1 || jb.kind == 0) gemm_tile<T0>(a, jb, t, qlds);
+  else gemm_tile<T1>(a, jb, t, qlds);
+}
+
+// Sum of the split-K partials part[z][tok][rows_total] in split order into each job's rows
+// (accumulate: added to y).
+__global__ __launch_bounds__(256) void k_gemm_reduce(QGemm a, uint32_t splits) {
+  const uint64_t n = (uint64_t)a.rows_total * a.batch;
   for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
     float v = 0.f;
-    for (uint32_t z = 0; z < splits; z++) v += part[(uint64_t)z * n + i];
-    const uint32_t tok = (uint32_t)(i / rows), row = (uint32_t)(i % rows);
-    float *py = y + (uint64_t)tok * stride + row_base + row;
-    *py = accumulate ? *py + v : v;
+    for (uint32_t z = 0; z < splits; z++) v += a.part[(uint64_t)z * n + i];
+    const uint32_t tok = (uint32_t)(i / a.rows_total);
+    uint32_t r = (uint32_t)(i % a.rows_total), j = 0;
+    while (j + 1 < a.njobs && r >= a.job[j].rows) { r -= a.job[j].rows; j++; }
+    float *py = a.job[j].y + (uint64_t)tok * a.job[j].stride + a.job[j].row_base + r;
+    *py = a.accumulate ? *py + v : v;
   }
+}
+
+// gate (rows [0, R)) and up (rows [R, 2R)) from the split-K partials, then act(gate) * up
+// into y [batch][R] and its split form for the down GEMM: one thread per eight columns of a
+// token.
+__global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t splits, uint32_t R, uint32_t batch,
+                                                    float *y, uint16_t *xs, int act) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= batch * (R / 8)) return;
+  const uint32_t tok = i / (R / 8), k = (i % (R / 8)) * 8;
+  const uint64_t n = (uint64_t)2 * R * batch, row = (uint64_t)tok * 2 * R;
+  float g[8] = {0, 0, 0, 0, 0, 0, 0, 0}, u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (uint32_t z = 0; z < splits; z++) {
+    const float *pg = part + z * n + row + k, *pu = pg + R;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const float4 a = *(const float4 *)(pg + 4 * h), b = *(const float4 *)(pu + 4 * h);
+      g[4 * h] += a.x; g[4 * h + 1] += a.y; g[4 * h + 2] += a.z; g[4 * h + 3] += a.w;
+      u[4 * h] += b.x; u[4 * h + 1] += b.y; u[4 * h + 2] += b.z; u[4 * h + 3] += b.w;
+    }
+  }
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = glu_act(g[e], act) * u[e];
+  const float4 a = make_float4(v[0], v[1], v[2], v[3]), b = make_float4(v[4], v[5], v[6], v[7]);
+  *(float4 *)(y + (uint64_t)tok * R + k) = a;
+  *(float4 *)(y + (uint64_t)tok * R + k + 4) = b;
+  split_store8(xs, R, tok, k, a, b);
 }
 
 static bool qgemm_supported(const Matrix &w) {
@@ -417,27 +465,67 @@ static bool qgemm_supported(const Matrix &w) {
   return w.type == Q8_0 && w.cols % QG_K == 0;
 }
 
+// The launch's two weight types (t[0] <= t[1]); false for more than two.
+static bool group_types(const GemmGroup &g, int t[2]) {
+  t[0] = t[1] = -1;
+  for (uint32_t j = 0; j < g.n; j++) {
+    const int ty = g.job[j].w->type;
+    if (ty == t[0] || ty == t[1]) continue;
+    if (t[0] < 0) t[0] = ty;
+    else if (t[1] < 0) t[1] = ty;
+    else return false;
+  }
+  if (t[1] < 0) t[1] = t[0];
+  if (t[0] > t[1]) std::swap(t[0], t[1]);
+  return true;
+}
+
+bool gemm_group_ok(const GemmGroup &g, uint32_t batch) {
+  if (!g.n || g.n > QG_MAX_JOBS || !batch) return false;
+  for (uint32_t j = 0; j < g.n; j++)
+    if (!g.job[j].w || !g.job[j].w->data || !qgemm_supported(*g.job[j].w) || g.job[j].w->cols != g.job[0].w->cols)
+      return false;
+  if (g.glu_out && (g.n != 2 || g.job[0].w->rows != g.job[1].w->rows || g.job[0].w->rows % QG_K)) return false;
+  int t[2];
+  return group_types(g, t);
+}
+
 // K span per workgroup: enough splits for two workgroups per CU (64 KB of LDS each), each
-// at least one 256-column block (64 columns for Q8_0), and no more partial sums than the
-// scratch holds.
-static uint32_t qgemm_kspan(const Matrix &w, uint32_t batch, uint64_t scratch_floats) {
-  const uint32_t align = w.type == Q8_0 ? QG_K : 256;
-  const uint32_t tiles = ((w.rows + QG_M - 1) / QG_M) * ((batch + QG_N - 1) / QG_N);
-  const uint32_t target = 2 * (uint32_t)device_cu_count();
+// at least one 256-column block (64 columns when every matrix is Q8_0), and no more partial
+// sums than the scratch holds.
+static uint32_t group_kspan(const GemmGroup &g, uint32_t batch, uint64_t scratch_floats, uint32_t *rows_total) {
+  uint32_t align = QG_K, tiles = 0, rows = 0;
+  for (uint32_t j = 0; j < g.n; j++) {
+    const Matrix &w = *g.job[j].w;
+    if (w.type != Q8_0) align = 256;
+    tiles += (w.rows + QG_M - 1) / QG_M;
+    rows += w.rows;
+  }
+  tiles *= (batch + QG_N - 1) / QG_N;
+  *rows_total = rows;
+  const uint32_t cols = g.job[0].w->cols, target = 2 * (uint32_t)device_cu_count();
   uint32_t splits = tiles >= target ? 1 : target / tiles;
-  const uint32_t units = w.cols / align;
+  const uint32_t units = cols / align;
   if (splits > units) splits = units;
   if (splits > 16) splits = 16;
-  while (splits > 1 && (uint64_t)splits * batch * w.rows > scratch_floats) splits--;
+  while (splits > 1 && (uint64_t)splits * batch * rows > scratch_floats) splits--;
   const uint32_t per = (units + splits - 1) / splits;
   return per * align;
 }
 
+uint64_t gemm_group_split_floats(const GemmGroup &g, uint32_t batch) {
+  if (!gemm_group_ok(g, batch)) return 0;
+  uint32_t rows = 0;
+  const uint32_t kspan = group_kspan(g, batch, ~0ull, &rows);
+  const uint32_t splits = (g.job[0].w->cols + kspan - 1) / kspan;
+  // the GLU finish reads its partials whole, so it always has room for them
+  return splits > 1 || g.glu_out ? (uint64_t)splits * batch * rows : 0;
+}
+
 uint64_t gemm_split_floats(const Matrix &w, uint32_t batch) {
-  if (!qgemm_supported(w) || !batch) return 0;
-  const uint32_t kspan = qgemm_kspan(w, batch, ~0ull);
-  const uint32_t splits = (w.cols + kspan - 1) / kspan;
-  return splits > 1 ? (uint64_t)splits * batch * w.rows : 0;
+  GemmGroup g;
+  g.job[0].w = &w; g.n = 1;
+  return gemm_group_split_floats(g, batch);
 }
 
 uint64_t gemm_input_elems(uint32_t cols, uint32_t batch) {
@@ -448,45 +536,86 @@ bool gemm_splits_input(const Matrix &w, const GemmScratch *scratch, uint32_t bat
   return qgemm_supported(w) && scratch && scratch->xs && scratch->xs_elems >= gemm_input_elems(w.cols, batch);
 }
 
+template <int T0, int T1>
+static void launch_qgemm(hipStream_t s, dim3 grid, const QGemm &q) {
+  static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
+  if (!big) {
+    (void)hipFuncSetAttribute((const void *)k_gemm_q<T0, T1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)QG_LDS);
+    big = true;
+  }
+  hipLaunchKernelGGL((k_gemm_q<T0, T1>), grid, dim3(256), QG_LDS, s, q);
+}
+
+hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_t batch, GemmScratch *scratch) {
+  if (!batch) return hipSuccess;
+  const uint32_t cols = g.job[0].w->cols;
+  if (!gemm_group_ok(g, batch) || !scratch || !scratch->xs || scratch->xs_elems < gemm_input_elems(cols, batch) ||
+      (uintptr_t)x % 16)
+    return hipErrorInvalidValue;
+  if (g.glu_out && (scratch->xs_elems < gemm_input_elems(g.job[0].w->rows, batch) || (uintptr_t)g.glu_out % 16))
+    return hipErrorInvalidValue;
+  if (scratch->xs_of != x || scratch->xs_cols != cols || scratch->xs_batch != batch) {
+    const uint32_t count = (uint32_t)(gemm_input_elems(cols, batch) / 16);
+    hipLaunchKernelGGL(k_gemm_split, dim3((count + 255) / 256), dim3(256), 0, s, x, scratch->xs, cols, batch, count);
+    WGD_HIP(hipGetLastError());
+    scratch->xs_of = x; scratch->xs_cols = cols; scratch->xs_batch = batch;
+  }
+  int types[2];
+  group_types(g, types);
+  QGemm q{};
+  q.njobs = g.n; q.xs = scratch->xs; q.cols = cols; q.batch = batch; q.accumulate = g.accumulate ? 1u : 0u;
+  uint32_t tiles = 0, row0 = 0;
+  for (uint32_t j = 0; j < g.n; j++) {
+    const Matrix &w = *g.job[j].w;
+    const uint64_t wbytes = planar_bytes(w.type, w.cols, w.rows);
+    if (wbytes >= (1ull << 31)) return hipErrorInvalidValue;
+    QJob &jb = q.job[j];
+    jb.w = w.data; jb.wbytes = (uint32_t)wbytes;
+    jb.C = w.cols / chunk_elems(w.type); jb.bpr = w.cols / block_size(w.type); jb.nbp = jb.bpr * (uint32_t)tile_rows(w.rows);
+    jb.rows = w.rows; jb.tiles = (w.rows + QG_M - 1) / QG_M; jb.kind = w.type == types[0] ? 0u : 1u; jb.row0 = row0;
+    jb.y = g.job[j].y; jb.stride = g.job[j].stride; jb.row_base = g.job[j].row_base;
+    tiles += jb.tiles; row0 += w.rows;
+  }
+  q.kspan = group_kspan(g, batch, scratch->p ? scratch->floats : 0, &q.rows_total);
+  const uint32_t splits = (cols + q.kspan - 1) / q.kspan;
+  // the GLU finish always reduces from the partials (a single split too)
+  const bool partials = splits > 1 || g.glu_out;
+  if (partials && (!scratch->p || (uint64_t)splits * batch * q.rows_total > scratch->floats)) return hipErrorInvalidValue;
+  q.part = partials ? scratch->p : nullptr;
+  const dim3 grid(tiles, (batch + QG_N - 1) / QG_N, splits);
+  const int a = types[0], b = types[1];
+  if (a == Q4_K && b == Q4_K) launch_qgemm<Q4_K, Q4_K>(s, grid, q);
+  else if (a == Q6_K && b == Q6_K) launch_qgemm<Q6_K, Q6_K>(s, grid, q);
+  else if (a == Q8_0 && b == Q8_0) launch_qgemm<Q8_0, Q8_0>(s, grid, q);
+  else if (a == Q4_K && b == Q6_K) launch_qgemm<Q4_K, Q6_K>(s, grid, q);
+  else if (a == Q8_0 && b == Q4_K) launch_qgemm<Q8_0, Q4_K>(s, grid, q);
+  else if (a == Q8_0 && b == Q6_K) launch_qgemm<Q8_0, Q6_K>(s, grid, q);
+  else return hipErrorInvalidValue;
+  WGD_HIP(hipGetLastError());
+  if (g.glu_out) {
+    const uint32_t R = g.job[0].w->rows, count = batch * (R / 8);
+    hipLaunchKernelGGL(k_glu_reduce, dim3((count + 255) / 256), dim3(256), 0, s, (const float *)q.part, splits, R, batch,
+                       g.glu_out, scratch->xs, g.glu_act);
+    WGD_HIP(hipGetLastError());
+    scratch->xs_of = g.glu_out; scratch->xs_cols = R; scratch->xs_batch = batch;
+  } else if (splits > 1) {
+    const uint64_t n = (uint64_t)q.rows_total * batch;
+    uint32_t blocks = (uint32_t)((n + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(256), 0, s, q, splits);
+  }
+  return hipGetLastError();
+}
+
 hipError_t gemm(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,
                 uint32_t row_base, uint32_t input_offset, uint32_t batch, GemmScratch *scratch, bool accumulate) {
   if (!w.rows || !batch) return hipSuccess;
   const float *xb = x + (uint64_t)input_offset * w.cols;
   if (gemm_splits_input(w, scratch, batch) && (uintptr_t)xb % 16 == 0) {
-    const uint64_t wbytes = planar_bytes(w.type, w.cols, w.rows);
-    if (wbytes >= (1ull << 31)) return hipErrorInvalidValue;
-    if (scratch->xs_of != xb || scratch->xs_cols != w.cols || scratch->xs_batch != batch) {
-      const uint32_t count = (uint32_t)(gemm_input_elems(w.cols, batch) / 16);
-      hipLaunchKernelGGL(k_gemm_split, dim3((count + 255) / 256), dim3(256), 0, s, xb, scratch->xs, w.cols, batch, count);
-      WGD_HIP(hipGetLastError());
-      scratch->xs_of = xb; scratch->xs_cols = w.cols; scratch->xs_batch = batch;
-    }
-    QGemm q;
-    q.w = w.data; q.wbytes = (uint32_t)wbytes;
-    q.C = w.cols / chunk_elems(w.type); q.bpr = w.cols / block_size(w.type); q.nbp = q.bpr * (uint32_t)tile_rows(w.rows);
-    q.xs = scratch->xs; q.y = y; q.cols = w.cols; q.rows = w.rows; q.stride = stride; q.row_base = row_base;
-    q.batch = batch; q.accumulate = accumulate ? 1u : 0u;
-    q.kspan = qgemm_kspan(w, batch, scratch->p ? scratch->floats : 0);
-    const uint32_t splits = (w.cols + q.kspan - 1) / q.kspan;
-    q.part = splits > 1 ? scratch->p : nullptr;
-    const dim3 grid((w.rows + QG_M - 1) / QG_M, (batch + QG_N - 1) / QG_N, splits);
-    auto go = [&](auto kernel) {
-      static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
-      if (!big) { (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)QG_LDS); big = true; }
-      hipLaunchKernelGGL(kernel, grid, dim3(256), QG_LDS, s, q);
-    };
-    if (w.type == Q4_K) go(k_gemm_q<Q4_K>);
-    else if (w.type == Q6_K) go(k_gemm_q<Q6_K>);
-    else go(k_gemm_q<Q8_0>);
-    WGD_HIP(hipGetLastError());
-    if (splits > 1) {
-      const uint64_t n = (uint64_t)w.rows * batch;
-      uint32_t blocks = (uint32_t)((n + 255) / 256);
-      if (blocks > 4096) blocks = 4096;
-      hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(256), 0, s, (const float *)q.part, y, w.rows, batch, splits,
-                         stride, row_base, q.accumulate);
-    }
-    return hipGetLastError();
+    GemmGroup g;
+    g.job[0] = GemmJob{&w, y, stride, row_base};
+    g.n = 1; g.accumulate = accumulate;
+    return gemm_group(s, g, xb, batch, scratch);
   }
   if (accumulate) return hipErrorInvalidValue;  // only the planar-weight GEMM adds into y
   if (w.cols % KT) return hipErrorInvalidValue;

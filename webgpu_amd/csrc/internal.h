@@ -81,6 +81,21 @@ uint64_t gemm_input_elems(uint32_t cols, uint32_t batch);
 // True when a GEMM of w over `batch` tokens runs the planar-weight kernel on the split input
 // (and may add into y).
 bool gemm_splits_input(const Matrix &w, const GemmScratch *scratch, uint32_t batch);
+
+// Up to three planar matrices with the same columns (at most two weight types) that read
+// the same activations, in one launch: y_j[b*stride_j + row_base_j + r] = W_j x_b, or
+// += with accumulate. glu_out (two jobs of equal rows: gate, up): act(gate) * up is written
+// there, [batch][rows], and its split into scratch->xs for the GEMM that reads it; the
+// jobs' own y are not written.
+struct GemmJob { const Matrix *w = nullptr; float *y = nullptr; uint32_t stride = 0, row_base = 0; };
+struct GemmGroup {
+  GemmJob job[3]; uint32_t n = 0;
+  bool accumulate = false;
+  float *glu_out = nullptr; int glu_act = 0;
+};
+bool gemm_group_ok(const GemmGroup &g, uint32_t batch);
+uint64_t gemm_group_split_floats(const GemmGroup &g, uint32_t batch);
+hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_t batch, GemmScratch *scratch);
 // y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]: the
 // generic kernel for small batches of GGUF-layout weights, else the MFMA dequant-GEMM.
 // accumulate (planar weights with split-input scratch only): y[...] += the sum.

@@ -157,6 +157,27 @@ hipError_t decode_attention_layer(wgd_model *m, int l, const QXOut &qx) {
   return decode_attention(m->ctx->stream, a);
 }
 
+// The prompt GEMM groups of a layer: Q, K and V of the normed input in one launch, and gate
+// with up finishing in the GLU (prod and its split for the down GEMM).
+static GemmGroup qkv_group(wgd_model *m, const Layer &L) {
+  const wgd_model_config &c = m->c;
+  const uint32_t qd = c.heads * c.head_dim, kd = c.kv_heads * c.head_dim;
+  GemmGroup g;
+  g.job[0] = GemmJob{&L.q, m->q, qd, 0};
+  g.job[1] = GemmJob{&L.k, m->k, kd, 0};
+  g.job[2] = GemmJob{&L.v, m->v, kd, 0};
+  g.n = 3;
+  return g;
+}
+static GemmGroup glu_group(wgd_model *m, const Layer &L) {
+  const uint32_t F = m->c.intermediate;
+  GemmGroup g;
+  g.job[0] = GemmJob{&L.gate, m->gate, F, 0};
+  g.job[1] = GemmJob{&L.up, m->up, F, 0};
+  g.n = 2; g.glu_out = m->prod; g.glu_act = m->c.gelu;
+  return g;
+}
+
 // n tokens already gathered into m->hidden (a prompt chunk, or one decode token on the
 // generic path with its position in device memory).
 hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_t *start_dev = nullptr) {
@@ -180,11 +201,16 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
     WGD_HIP(norm_for(L.attn_norm, L.q));
-    WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, &gs));
+    const GemmGroup qkv = qkv_group(m, L);
+    if (gemm_splits_input(L.q, &gs, n) && gemm_group_ok(qkv, n)) {
+      WGD_HIP(gemm_group(s, qkv, m->normed, n, &gs));
+    } else {
+      WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, &gs));
+      WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, &gs));
+      WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, n, &gs));
+    }
     WGD_HIP(bias(s, m->q, L.bq, n, qd));
-    WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->k, L.bk, n, kd));
-    WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, n, &gs));
     WGD_HIP(bias(s, m->v, L.bv, n, kd));
     WGD_HIP(attention_block(m, l, n, start, start_dev));
     gs.xs_of = nullptr;
@@ -197,9 +223,13 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       else WGD_HIP(add(s, m->proj, m->hidden, n * H));
     }
     WGD_HIP(norm_for(L.ffn_norm, L.up));
-    WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, n, &gs));
     float *ffn_in = m->up;
-    if (c.ffn_gate) {
+    const GemmGroup gu = glu_group(m, L);
+    if (c.ffn_gate && gemm_splits_input(L.up, &gs, n) && gemm_group_ok(gu, n)) {
+      WGD_HIP(gemm_group(s, gu, m->normed, n, &gs));  // leaves the split of prod in gs.xs
+      ffn_in = m->prod;
+    } else if (c.ffn_gate) {
+      WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, n, &gs));
       WGD_HIP(matmul(s, L.gate, m->normed, m->gate, F, 0, 0, n, &gs));
       if (gemm_splits_input(L.down, &gs, n)) {
         WGD_HIP(glu_split(s, m->gate, m->up, m->prod, gs.xs, F, n, c.gelu));
@@ -210,6 +240,7 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       }
       ffn_in = m->prod;
     } else {
+      WGD_HIP(matmul(s, L.up, m->normed, m->up, F, 0, 0, n, &gs));
       WGD_HIP(activate(s, m->up, n * F));
       gs.xs_of = nullptr;
     }
@@ -606,12 +637,15 @@ int wgd_model_ready(wgd_model *m) {
   // prompt GEMM scratch: split-K sums and the bf16 split input, the most any layer matrix
   // uses at the batch size
   uint64_t gp = 0, gx = 0;
-  for (const Layer &L : m->L)
+  for (const Layer &L : m->L) {
     for (const Matrix *w : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
       if (w->data) {
         gp = std::max(gp, gemm_split_floats(*w, (uint32_t)c.batch));
         gx = std::max(gx, gemm_input_elems(w->cols, (uint32_t)c.batch));
       }
+    gp = std::max(gp, gemm_group_split_floats(qkv_group(m, L), (uint32_t)c.batch));
+    if (c.ffn_gate) gp = std::max(gp, gemm_group_split_floats(glu_group(m, L), (uint32_t)c.batch));
+  }
   if (gp && !m->gemm_part.p) {
     rc = alloc_t(m, gp, "prompt GEMM split sums", &m->gemm_part.p);
     if (rc) return rc;

@@ -145,13 +145,10 @@ hipError_t rope(hipStream_t s, float *x, const float *w, uint32_t heads, uint32_
 __global__ void k_add(const float *d, float *state, uint32_t n) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) state[i] += d[i];
 }
-__device__ __forceinline__ float gelu_tanh_f(float g) {
-  return 0.5f * g * (1.f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g)));
-}
 __global__ void k_glu(const float *g, const float *u, float *y, uint32_t n, int act) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     float x = g[i];
-    y[i] = (act ? gelu_tanh_f(x) : x / (1.f + expf(-x))) * u[i];
+    y[i] = glu_act(x, act) * u[i];
   }
 }
 __global__ void k_bias(float *y, const float *b, uint32_t n, uint32_t width) {
@@ -189,7 +186,7 @@ __global__ __launch_bounds__(256) void k_glu_split(const float *g, const float *
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const float x = gg[e];
-      v[4 * h + e] = (act ? gelu_tanh_f(x) : x / (1.f + expf(-x))) * uu[e];
+      v[4 * h + e] = glu_act(x, act) * uu[e];
     }
   }
   const float4 a = make_float4(v[0], v[1], v[2], v[3]), b = make_float4(v[4], v[5], v[6], v[7]);

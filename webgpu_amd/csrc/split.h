@@ -33,6 +33,12 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - back, bf16x2));
 }
 
+// The gate activations of the GLU: SiLU (act 0) and tanh-approximated GELU (act 1).
+__device__ __forceinline__ float glu_act(float x, int act) {
+  if (!act) return x / (1.f + expf(-x));
+  return 0.5f * x * (1.f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+}
+
 // Columns k..k+7 (k % 8 == 0) of token tok.
 __device__ __forceinline__ void split_store8(uint16_t *xs, uint32_t cols, uint32_t tok, uint32_t k, float4 a, float4 b) {
   uint32_t h[4], l[4];
