@@ -246,18 +246,24 @@ def main() -> None:
     print(f"[bench] loaded in {time.perf_counter() - t:.1f} s on {eng.gpu.adapterName}", file=sys.stderr, flush=True)
     ids = synth.prompt_ids(eng.config.vocab, a.prompt, seed=7)
 
-    # prefill (reported, not the metric)
-    eng.gpu.done()
-    t = time.perf_counter()
-    for i in range(0, a.prompt, 128):
-        chunk = ids[i:i + 128]
-        if i + len(chunk) == a.prompt:
-            token = eng.forward_argmax(chunk, i)
-        else:
-            eng.forward(chunk, i, False)
-    eng.gpu.done()
-    prefill_s = time.perf_counter() - t
-    print(f"[bench] prefill {a.prompt} tokens in {prefill_s * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    # prefill (reported, not the metric): one untimed pass loads every kernel, then the median
+    # of three timed passes over the same positions (each rewrites the same KV slots)
+    def prefill():
+        eng.gpu.done()
+        t = time.perf_counter()
+        for i in range(0, a.prompt, 128):
+            chunk = ids[i:i + 128]
+            if i + len(chunk) == a.prompt:
+                tok = eng.forward_argmax(chunk, i)
+            else:
+                eng.forward(chunk, i, False)
+        eng.gpu.done()
+        return time.perf_counter() - t, tok
+    prefill()
+    runs = [prefill() for _ in range(3)]
+    prefill_s, token = sorted(runs)[1]
+    print(f"[bench] prefill {a.prompt} tokens in {prefill_s * 1e3:.1f} ms (median of 3 after a warm-up pass)",
+          file=sys.stderr, flush=True)
 
     pos = a.prompt
     if a.warmup:

@@ -261,8 +261,15 @@ hipError_t head(wgd_model *m, uint32_t row) {
   const wgd_model_config &c = m->c;
   hipStream_t s = m->ctx->stream;
   const Matrix &W = m->have_output && !c.tied_output ? m->output : m->embd;
-  WGD_HIP(norm(s, m->hidden + (uint64_t)row * c.hidden, m->out_norm, m->normed, c.hidden, c.epsilon, 1));
-  WGD_HIP(matmul(s, W, m->normed, m->logits, c.vocab, 0, 0, 1));
+  if (m->qpath && m->qx_head) {
+    // the decode head: the row quantized with the output norm pending, then the integer matvec
+    const QXOut q = qx_view(m->qx_head, c.hidden);
+    WGD_HIP(quantize(s, m->hidden + (uint64_t)row * c.hidden, c.hidden, m->out_norm, q));
+    WGD_HIP(mv(s, W, nullptr, qx_const(q, c.hidden, true, c.epsilon), m->logits, MV_STORE));
+  } else {
+    WGD_HIP(norm(s, m->hidden + (uint64_t)row * c.hidden, m->out_norm, m->normed, c.hidden, c.epsilon, 1));
+    WGD_HIP(matmul(s, W, m->normed, m->logits, c.vocab, 0, 0, 1));
+  }
   return argmax(s, m->logits, c.vocab, m->argmax_buf);
 }
 
