@@ -15,9 +15,11 @@ time. traffic = HBM bytes per launch from the committed rocprofv3 counter summar
 same microbench (profiles/k_mv_matvec_microbench.md). The other microbench shapes (4096x4096,
 4096x14336 Q4_K; 4096x128256 Q6_K) are reported under "matvec".
 
-prefill_gemm: the prompt-batch dequant-GEMM at the 8B layer shapes with 128 tokens, timed
-with HIP events; its MFMA utilisation counts the three bf16 MFMAs per product of the
-hi/lo operand split against the 2.5 PFLOP/s dense bf16 peak.
+prefill_tok_s: the 512-token prompt after one untimed pass, median of three passes.
+prefill_gemm: the prompt-batch dequant-GEMM at the 8B layer shapes with 128 tokens as
+single-matrix wgd_matmul calls (input split, GEMM and split-K reduction), timed with HIP
+events; its MFMA utilisation counts the three bf16 MFMAs per product of the hi/lo operand
+split against the 2.5 PFLOP/s dense bf16 peak.
 
 cpu_baseline: the float64 C oracle (OpenMP over the host cores) decoding the same 8B
 model on a bounded sample (8-token prompt, then as many greedy tokens as fit ~15 s).
