@@ -23,6 +23,10 @@ split against the 2.5 PFLOP/s dense bf16 peak.
 
 cpu_baseline: the float64 C oracle (OpenMP over the host cores) decoding the same 8B
 model on a bounded sample (8-token prompt, then as many greedy tokens as fit ~15 s).
+
+--model qwen3-0.6b / gemma3-27b run the other shaped decoders (64-token prompt and 256
+tokens; 8192-token prompt in 64 batches and 128 tokens at context 8448) with the same
+JSON line; the default is the headline workload above.
 """
 from __future__ import annotations
 
@@ -62,6 +66,15 @@ def profiled_traffic(type_name: str, shape: str):
         pass
     return None
 METRIC = "decode tok/s (1 GPU) + Q4_K matvec HBM GB/s as % of peak"
+
+# Workloads: the default (the headline) and the other shaped decoders, each with its prompt,
+# decode length and context (a prompt of `prompt` tokens in 128-token batches, then `steps`
+# greedy tokens).
+WORKLOADS = {
+    "llama3-8b": dict(prompt=512, steps=256, context=1024, title="Llama-3-8B-shaped Q4_K_M"),
+    "qwen3-0.6b": dict(prompt=64, steps=256, context=1024, title="Qwen3-0.6B-shaped Q4_K_M"),
+    "gemma3-27b": dict(prompt=8192, steps=128, context=8448, title="Gemma-3-27B-shaped Q4_K_M"),
+}
 
 
 class Events:
@@ -173,7 +186,7 @@ def gemm_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, batch
             "tflops": flops / t / 1e12, "mfma_tflops": 3 * flops / t / 1e12, "mfma_frac": 3 * flops / t / PEAK_BF16}
 
 
-def cpu_baseline(f: np.ndarray, seconds: float = 15.0) -> dict:
+def cpu_baseline(f: np.ndarray, title: str, seconds: float = 15.0) -> dict:
     from oracle import orc
     from webgpu_amd.context import attention_memory
     from webgpu_amd.gguf import model_config, parse_gguf_header
@@ -189,16 +202,18 @@ def cpu_baseline(f: np.ndarray, seconds: float = 15.0) -> dict:
     dt = time.perf_counter() - t0
     m.close()
     return {"value": n / dt, "unit": "tok/s", "cores": orc.threads(), "kind": "port",
-            "sample": f"float64 C oracle, Llama-3-8B-shaped Q4_K_M decode: 8-token prompt then {n} greedy tokens "
+            "sample": f"float64 C oracle, {title} decode: 8-token prompt then {n} greedy tokens "
                       f"in {dt:.1f} s on {orc.threads()} threads ({platform.processor() or platform.machine()})"}
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--model", default="llama3-8b", choices=sorted(WORKLOADS),
+                    help="shaped decoder to run (the default is the headline workload)")
+    ap.add_argument("--steps", type=int, default=None, help="timed decode tokens (default: per model)")
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: per model)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-matvec", action="store_true", help="skip the matvec microbench")
     ap.add_argument("--matvec-only", action="store_true",
@@ -235,13 +250,20 @@ def main() -> None:
                   f"({g['mfma_tflops']:.0f} TFLOP/s of bf16 MFMA, {100 * g['mfma_frac']:.1f}% of peak)", file=sys.stderr, flush=True)
         gpu.dispose()
         return
-    context = 1024
+    wl = WORKLOADS[a.model]
+    if a.prompt is None:
+        a.prompt = wl["prompt"]
+    if a.steps is None:
+        a.steps = wl["steps"]
+    context = wl["context"]
     if a.prompt + a.warmup + a.steps > context:
         context = min(32768, 1 << (a.prompt + a.warmup + a.steps - 1).bit_length())
+    spec = synth.SPECS[a.model]
 
     t = time.perf_counter()
-    f = synth.build("llama3-8b")
-    print(f"[bench] synthetic 8B GGUF {f.size / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s", file=sys.stderr, flush=True)
+    f = synth.build(a.model)
+    print(f"[bench] synthetic {a.model} GGUF {f.size / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s",
+          file=sys.stderr, flush=True)
     eng = PagedEngine()
     t = time.perf_counter()
     eng.load(f, LoadOptions(contextLength=context, batchSize=128))
@@ -283,9 +305,10 @@ def main() -> None:
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": dt * 1e3 / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded random-init Q4_K_M GGUF)",
-        "config": {"workload": "llama3-8b-shape Q4_K_M greedy decode", "prompt": a.prompt, "prefill_batch": 128,
+        "config": {"workload": f"{a.model}-shape Q4_K_M greedy decode", "prompt": a.prompt, "prefill_batch": 128,
                    "decode_tokens": a.steps, "context": context, "kv_cache": "f32",
-                   "layers": 32, "hidden": 4096, "heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256},
+                   "layers": spec.layers, "hidden": spec.hidden, "heads": spec.heads, "kv_heads": spec.kv_heads,
+                   "ffn": spec.ffn, "vocab": spec.vocab},
         "prefill_tok_s": a.prompt / prefill_s,
     }
     eng.dispose()
@@ -311,7 +334,7 @@ def main() -> None:
             print(f"[bench] gemm {g['type']} {g['shape']} x {g['batch']} tokens: {g['us']:.1f} us, {g['tflops']:.0f} TFLOP/s "
                   f"({100 * g['mfma_frac']:.1f}% of bf16 MFMA peak)", file=sys.stderr, flush=True)
     if not a.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(f)
+        result["cpu_baseline"] = cpu_baseline(f, wl["title"])
         print(f"[bench] cpu baseline {result['cpu_baseline']['value']:.3f} tok/s", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
 

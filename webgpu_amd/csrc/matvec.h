@@ -77,6 +77,10 @@ __device__ __forceinline__ void qx_store(const QXOut &q, uint32_t i, float v, fl
 
 // x (length K, K % 16 == 0) -> QX; with norm_w the stored values are x * norm_w.
 hipError_t quantize(hipStream_t s, const float *x, uint32_t K, const float *norm_w, const QXOut &q);
+// One row: state += RMSNorm(delta) * w (Gemma's post-norms), then the QX of the new state
+// times next_w (n % 16 == 0), in one launch.
+hipError_t norm_add_quantize(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n, float eps,
+                             const float *next_w, const QXOut &q);
 
 enum MVEpilogue : int { MV_STORE = 0, MV_ADD = 1, MV_SILU = 2, MV_GELU = 3 };
 

@@ -369,8 +369,7 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
     } else {
       o.y = m->proj;
       WGD_HIP(mv(s, &o, 1, qv(m->qx_o, qd), MV_STORE));
-      WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, 1));
-      WGD_HIP(quantize(s, m->hidden, H, L.ffn_norm, to_ffn.q));
+      WGD_HIP(norm_add_quantize(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, L.ffn_norm, to_ffn.q));
     }
     MVOut to_down;
     to_down.q = qx_view(m->qx_down, F);
@@ -390,8 +389,7 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
       WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->hidden, MV_ADD, &next));
     } else {
       WGD_HIP(mv(s, L.down, nullptr, qv(m->qx_down, F), m->down, MV_STORE));
-      WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, 1));
-      WGD_HIP(quantize(s, m->hidden, H, next.norm_w, next.q));
+      WGD_HIP(norm_add_quantize(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, next.norm_w, next.q));
     }
   }
   const Matrix &W = m->have_output && !c.tied_output ? m->output : m->embd;

@@ -10,6 +10,7 @@
 #include "internal.h"
 #include "decode.h"
 #include "split.h"
+#include "matvec.h"
 
 namespace wgd {
 
@@ -87,9 +88,61 @@ __global__ __launch_bounds__(256) void k_norm_add(const float *d, const float *w
   for (uint32_t i = threadIdx.x; i < n; i += 256) sr[i] += dr[i] * inv * w[i];
 }
 
+// The same for rows of up to NA_T * NA_E elements: one 1024-thread workgroup per row with
+// every element loaded at once (the strided loop above is a chain of dependent round trips
+// at batch 1). With q.d0 set it also writes the QX form of the new state times next_w, the
+// input of the next projection with its RMSNorm pending (elements i + NA_T e: each 16-lane
+// group holds 16 consecutive elements).
+constexpr uint32_t NA_T = 1024, NA_E = 12;
+__global__ __launch_bounds__(1024) void k_norm_add_q(const float *d, const float *w, float *state, uint32_t n,
+                                                     float eps, const float *next_w, QXOut q) {
+  __shared__ float red[NA_T / 64];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float *dr = d + (uint64_t)blockIdx.x * n;
+  float *sr = state + (uint64_t)blockIdx.x * n;
+  float dv[NA_E], s = 0.f;
+#pragma unroll
+  for (uint32_t e = 0; e < NA_E; e++) {
+    const uint32_t i = tid + NA_T * e;
+    dv[e] = i < n ? dr[i] : 0.f;
+    s += dv[e] * dv[e];
+  }
+  s = wave_sum(s);
+  if (lane == 0) red[wv] = s;
+  __syncthreads();
+  s = 0.f;
+#pragma unroll
+  for (uint32_t u = 0; u < NA_T / 64; u++) s += red[u];
+  const float inv = 1.f / sqrtf(s / (float)n + eps);
+#pragma unroll
+  for (uint32_t e = 0; e < NA_E; e++) {
+    const uint32_t i = tid + NA_T * e;
+    if (NA_T * e >= n) break;  // uniform
+    const bool live = i < n;
+    const float nv = live ? sr[i] + dv[e] * inv * w[i] : 0.f;
+    if (live) sr[i] = nv;
+    if (q.d0) qx_store(q, i, live ? nv * next_w[i] : 0.f, nv, live);
+  }
+}
+
 hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n, float eps, uint32_t batch) {
   if (!batch || !n) return hipSuccess;
-  hipLaunchKernelGGL(k_norm_add, dim3(batch), dim3(256), 0, s, delta, w, state, n, eps);
+  if (n <= NA_T * NA_E) {
+    hipLaunchKernelGGL(k_norm_add_q, dim3(batch), dim3(NA_T), 0, s, delta, w, state, n, eps, (const float *)nullptr, QXOut());
+  } else {
+    hipLaunchKernelGGL(k_norm_add, dim3(batch), dim3(256), 0, s, delta, w, state, n, eps);
+  }
+  return hipGetLastError();
+}
+
+hipError_t norm_add_quantize(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n, float eps,
+                             const float *next_w, const QXOut &q) {
+  if (!n || n % 16 || !next_w) return hipErrorInvalidValue;
+  if (n > NA_T * NA_E) {
+    WGD_HIP(norm_add(s, delta, w, state, n, eps, 1));
+    return quantize(s, state, n, next_w, q);
+  }
+  hipLaunchKernelGGL(k_norm_add_q, dim3(1), dim3(NA_T), 0, s, delta, w, state, n, eps, next_w, q);
   return hipGetLastError();
 }
 
