@@ -518,8 +518,8 @@ uint64_t gemm_group_split_floats(const GemmGroup &g, uint32_t batch) {
   uint32_t rows = 0;
   const uint32_t kspan = group_kspan(g, batch, ~0ull, &rows);
   const uint32_t splits = (g.job[0].w->cols + kspan - 1) / kspan;
-  // the GLU finish reads its partials whole, so it always has room for them
-  return splits > 1 || g.glu_out ? (uint64_t)splits * batch * rows : 0;
+  // the GLU finish and a kept group read their partials whole, so they always have room
+  return splits > 1 || g.glu_out || g.keep_partials ? (uint64_t)splits * batch * rows : 0;
 }
 
 uint64_t gemm_split_floats(const Matrix &w, uint32_t batch) {
@@ -578,8 +578,8 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
   }
   q.kspan = group_kspan(g, batch, scratch->p ? scratch->floats : 0, &q.rows_total);
   const uint32_t splits = (cols + q.kspan - 1) / q.kspan;
-  // the GLU finish always reduces from the partials (a single split too)
-  const bool partials = splits > 1 || g.glu_out;
+  // the GLU finish and a kept group always reduce from the partials (a single split too)
+  const bool partials = splits > 1 || g.glu_out || g.keep_partials;
   if (partials && (!scratch->p || (uint64_t)splits * batch * q.rows_total > scratch->floats)) return hipErrorInvalidValue;
   q.part = partials ? scratch->p : nullptr;
   const dim3 grid(tiles, (batch + QG_N - 1) / QG_N, splits);
@@ -598,6 +598,8 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
                        g.glu_out, scratch->xs, g.glu_act);
     WGD_HIP(hipGetLastError());
     scratch->xs_of = g.glu_out; scratch->xs_cols = R; scratch->xs_batch = batch;
+  } else if (g.keep_partials) {
+    if (g.splits) *g.splits = splits;
   } else if (splits > 1) {
     const uint64_t n = (uint64_t)q.rows_total * batch;
     uint32_t blocks = (uint32_t)((n + 255) / 256);

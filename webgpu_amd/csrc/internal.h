@@ -92,6 +92,9 @@ struct GemmGroup {
   GemmJob job[3]; uint32_t n = 0;
   bool accumulate = false;
   float *glu_out = nullptr; int glu_act = 0;
+  // leave the split-K partials (one split too) in scratch->p for the caller's own finish;
+  // the number of splits is returned in *splits
+  bool keep_partials = false; uint32_t *splits = nullptr;
 };
 bool gemm_group_ok(const GemmGroup &g, uint32_t batch);
 uint64_t gemm_group_split_floats(const GemmGroup &g, uint32_t batch);
@@ -120,6 +123,22 @@ hipError_t norm_split(hipStream_t s, const float *x, const float *w, float *y, u
 hipError_t rope(hipStream_t s, float *x, const float *w, uint32_t heads, uint32_t hd,
                 uint32_t start, const int32_t *start_dev, float theta, float scale, float eps,
                 uint32_t rotary_dim, uint32_t batch, int mode);
+// The finish of a Q/K/V GEMM group kept as split-K partials (rows q | k | v per token):
+// sums, bias, RoPE (rope()'s modes), Q into q and K/V into ring slot (start + t) % capacity.
+struct QKVFinish {
+  const float *part = nullptr; uint32_t splits = 0, rows_total = 0, batch = 0;
+  const float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  const float *qn = nullptr, *kn = nullptr;  // mode 0 norm weights
+  float *q = nullptr, *kc = nullptr, *vc = nullptr; uint32_t capacity = 0;
+  uint32_t heads = 0, kvh = 0, hd = 0, rot = 0, start = 0; const int32_t *start_dev = nullptr;
+  float eps = 0.f; int mode = 1;
+  const float2 *cs = nullptr;  // rope_table() of the batch's positions
+};
+hipError_t qkv_finish(hipStream_t s, const QKVFinish &a);
+// cs[t * rot/2 + i] = (cos, sin) of (start + t) * scale * theta^(-2i/rot) for t < n (angles in
+// f64, as rope() forms them); start_dev overrides start.
+hipError_t rope_table(hipStream_t s, float2 *cs, uint32_t rot, uint32_t n, uint32_t start, const int32_t *start_dev,
+                      float theta, float scale);
 struct AttnArgs {
   const float *q; const float *k; const float *v; float *y;
   uint32_t heads, kv_heads, hd, start; const int32_t *start_dev;

@@ -75,6 +75,7 @@ struct wgd_model {
   // RoPE inverse frequencies of the decode attention: [0] the model's theta, [1] Gemma's local
   double *inv_freq[2] = {nullptr, nullptr};
   float *rope_cs[2] = {nullptr, nullptr};  // this token's rotation tables (token_start)
+  float2 *rope_batch[2] = {nullptr, nullptr};  // a prompt batch's rotations (rope_table)
   void *qx_attn = nullptr, *qx_ffn = nullptr, *qx_o = nullptr, *qx_down = nullptr, *qx_head = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -107,25 +108,34 @@ hipError_t bias(hipStream_t s, float *y, const float *b, uint32_t n, uint32_t wi
   return b ? bias_add(s, y, b, n * width, width) : hipSuccess;
 }
 
-// Attention + RoPE + KV append for one layer; positions from start (host) or start_dev.
-hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, const int32_t *start_dev) {
+// The RoPE of layer l: theta, scale, mode (0 Q/K norm + half-split, 1 half-split,
+// 2 adjacent), rotary width (0 = head dim) and norm epsilon.
+struct RopeParams { float theta, scale, eps; uint32_t rot; int mode; };
+static RopeParams rope_params(wgd_model *m, int l) {
+  const wgd_model_config &c = m->c;
+  if (is_gemma(m)) {
+    const bool loc = local_layer(m, l);
+    return RopeParams{loc ? c.local_theta : c.theta, loc ? 1.f : c.rope_scale, c.epsilon, 0, 0};
+  }
+  if (c.qk_norm) return RopeParams{c.theta, c.rope_scale, c.epsilon, (uint32_t)c.rotary_dim, 0};
+  return RopeParams{c.theta, c.rope_scale, 0.f, (uint32_t)c.rotary_dim, c.rope_adjacent ? 2 : 1};
+}
+
+// Attention of one layer, with RoPE and the KV append unless `prepared` (the Q/K/V GEMM
+// finish did them); positions from start (host) or start_dev.
+hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, const int32_t *start_dev,
+                           bool prepared = false) {
   const wgd_model_config &c = m->c;
   Layer &L = m->L[l];
   hipStream_t s = m->ctx->stream;
   const uint32_t hd = c.head_dim, kd = c.kv_heads * hd;
-  if (is_gemma(m)) {
-    float theta = local_layer(m, l) ? c.local_theta : c.theta, scale = local_layer(m, l) ? 1.f : c.rope_scale;
-    WGD_HIP(rope(s, m->q, L.q_norm, c.heads, hd, start, start_dev, theta, scale, c.epsilon, 0, n, 0));
-    WGD_HIP(rope(s, m->k, L.k_norm, c.kv_heads, hd, start, start_dev, theta, scale, c.epsilon, 0, n, 0));
-  } else if (c.qk_norm) {
-    WGD_HIP(rope(s, m->q, L.q_norm, c.heads, hd, start, start_dev, c.theta, c.rope_scale, c.epsilon, c.rotary_dim, n, 0));
-    WGD_HIP(rope(s, m->k, L.k_norm, c.kv_heads, hd, start, start_dev, c.theta, c.rope_scale, c.epsilon, c.rotary_dim, n, 0));
-  } else {
-    int mode = c.rope_adjacent ? 2 : 1;
-    WGD_HIP(rope(s, m->q, nullptr, c.heads, hd, start, start_dev, c.theta, c.rope_scale, 0.f, c.rotary_dim, n, mode));
-    WGD_HIP(rope(s, m->k, nullptr, c.kv_heads, hd, start, start_dev, c.theta, c.rope_scale, 0.f, c.rotary_dim, n, mode));
+  if (!prepared) {
+    const RopeParams r = rope_params(m, l);
+    const float *qn = r.mode == 0 ? L.q_norm : nullptr, *kn = r.mode == 0 ? L.k_norm : nullptr;
+    WGD_HIP(rope(s, m->q, qn, c.heads, hd, start, start_dev, r.theta, r.scale, r.eps, r.rot, n, r.mode));
+    WGD_HIP(rope(s, m->k, kn, c.kv_heads, hd, start, start_dev, r.theta, r.scale, r.eps, r.rot, n, r.mode));
+    WGD_HIP(kv_append(s, m->k, m->v, L.kc, L.vc, kd, n, start, start_dev, L.cap));
   }
-  WGD_HIP(kv_append(s, m->k, m->v, L.kc, L.vc, kd, n, start, start_dev, L.cap));
   AttnArgs a;
   a.q = m->q; a.k = L.kc; a.v = L.vc; a.y = m->att;
   a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = hd; a.start = start; a.start_dev = start_dev;
@@ -166,7 +176,7 @@ static GemmGroup qkv_group(wgd_model *m, const Layer &L) {
   g.job[0] = GemmJob{&L.q, m->q, qd, 0};
   g.job[1] = GemmJob{&L.k, m->k, kd, 0};
   g.job[2] = GemmJob{&L.v, m->v, kd, 0};
-  g.n = 3;
+  g.n = 3; g.keep_partials = true;
   return g;
 }
 static GemmGroup glu_group(wgd_model *m, const Layer &L) {
@@ -198,21 +208,48 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
     return norm_split(s, m->hidden, w, m->normed, gs.xs, H, c.epsilon, n);
   };
   const bool gemma = is_gemma(m);
+  // the batch's RoPE rotations, once for every layer (Gemma: global and local theta)
+  if (m->rope_batch[0]) {
+    int lg = 0, ll = 0;  // a global and a local layer (Gemma)
+    while (lg + 1 < c.layers && local_layer(m, lg)) lg++;
+    while (ll + 1 < c.layers && !local_layer(m, ll)) ll++;
+    const RopeParams r0 = rope_params(m, lg);
+    WGD_HIP(rope_table(s, m->rope_batch[0], r0.rot ? r0.rot : c.head_dim, n, start, start_dev, r0.theta, r0.scale));
+    if (gemma && m->rope_batch[1]) {
+      const RopeParams r1 = rope_params(m, ll);
+      WGD_HIP(rope_table(s, m->rope_batch[1], c.head_dim, n, start, start_dev, r1.theta, r1.scale));
+    }
+  }
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
     WGD_HIP(norm_for(L.attn_norm, L.q));
-    const GemmGroup qkv = qkv_group(m, L);
-    if (gemm_splits_input(L.q, &gs, n) && gemm_group_ok(qkv, n)) {
+    GemmGroup qkv = qkv_group(m, L);
+    uint32_t splits = 0;
+    qkv.keep_partials = true; qkv.splits = &splits;
+    if (m->rope_batch[0] && gemm_splits_input(L.q, &gs, n) && gemm_group_ok(qkv, n)) {
+      // Q/K/V partial sums finished in one pass: bias, RoPE, K/V into the ring
       WGD_HIP(gemm_group(s, qkv, m->normed, n, &gs));
+      const RopeParams r = rope_params(m, l);
+      QKVFinish f;
+      f.part = gs.p; f.splits = splits; f.rows_total = qd + 2 * kd; f.batch = n;
+      f.bq = L.bq; f.bk = L.bk; f.bv = L.bv;
+      f.qn = r.mode == 0 ? L.q_norm : nullptr; f.kn = r.mode == 0 ? L.k_norm : nullptr;
+      f.q = m->q; f.kc = L.kc; f.vc = L.vc; f.capacity = L.cap;
+      f.heads = c.heads; f.kvh = c.kv_heads; f.hd = c.head_dim; f.rot = r.rot ? r.rot : c.head_dim;
+      f.start = start; f.start_dev = start_dev;
+      f.eps = r.eps; f.mode = r.mode;
+      f.cs = m->rope_batch[gemma && local_layer(m, l) ? 1 : 0];
+      WGD_HIP(qkv_finish(s, f));
+      WGD_HIP(attention_block(m, l, n, start, start_dev, true));
     } else {
       WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, &gs));
       WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, &gs));
       WGD_HIP(matmul(s, L.v, m->normed, m->v, kd, 0, 0, n, &gs));
+      WGD_HIP(bias(s, m->q, L.bq, n, qd));
+      WGD_HIP(bias(s, m->k, L.bk, n, kd));
+      WGD_HIP(bias(s, m->v, L.bv, n, kd));
+      WGD_HIP(attention_block(m, l, n, start, start_dev));
     }
-    WGD_HIP(bias(s, m->q, L.bq, n, qd));
-    WGD_HIP(bias(s, m->k, L.bk, n, kd));
-    WGD_HIP(bias(s, m->v, L.bv, n, kd));
-    WGD_HIP(attention_block(m, l, n, start, start_dev));
     gs.xs_of = nullptr;
     if (!gemma && !L.bo && gemm_splits_input(L.o, &gs, n)) {
       WGD_HIP(matmul(s, L.o, m->att, m->hidden, H, 0, 0, n, &gs, true));
@@ -660,6 +697,14 @@ int wgd_model_ready(wgd_model *m) {
     rc = alloc_t(m, gx, "prompt GEMM split input", &m->gemm_part.xs);
     if (rc) return rc;
     m->gemm_part.xs_elems = gx;
+  }
+  // a prompt batch's RoPE rotations (the model's theta; Gemma's local theta too)
+  if (!m->rope_batch[0]) {
+    const uint32_t rot = is_gemma(m) || !c.rotary_dim ? (uint32_t)c.head_dim : (uint32_t)c.rotary_dim;
+    const uint64_t entries = (uint64_t)c.batch * (rot / 2);
+    rc = alloc_t(m, entries, "rope batch table", &m->rope_batch[0]);
+    if (!rc && is_gemma(m)) rc = alloc_t(m, entries, "rope batch table (local)", &m->rope_batch[1]);
+    if (rc) return rc;
   }
   // The quantized decode path needs every matrix in a type the integer matvec reads.
   const Matrix &head_w = m->have_output && !c.tied_output ? m->output : m->embd;

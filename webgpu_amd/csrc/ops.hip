@@ -100,13 +100,19 @@ __global__ __launch_bounds__(1024) void k_norm_add_q(const float *d, const float
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const float *dr = d + (uint64_t)blockIdx.x * n;
   float *sr = state + (uint64_t)blockIdx.x * n;
-  float dv[NA_E], s = 0.f;
+  // every load goes out before the reduction: one round trip per launch
+  float dv[NA_E], sv[NA_E], wv_[NA_E], nw[NA_E], s = 0.f;
 #pragma unroll
   for (uint32_t e = 0; e < NA_E; e++) {
     const uint32_t i = tid + NA_T * e;
-    dv[e] = i < n ? dr[i] : 0.f;
-    s += dv[e] * dv[e];
+    const bool live = i < n;
+    dv[e] = live ? dr[i] : 0.f;
+    sv[e] = live ? sr[i] : 0.f;
+    wv_[e] = live ? w[i] : 0.f;
+    nw[e] = live && next_w ? next_w[i] : 0.f;
   }
+#pragma unroll
+  for (uint32_t e = 0; e < NA_E; e++) s += dv[e] * dv[e];
   s = wave_sum(s);
   if (lane == 0) red[wv] = s;
   __syncthreads();
@@ -119,9 +125,9 @@ __global__ __launch_bounds__(1024) void k_norm_add_q(const float *d, const float
     const uint32_t i = tid + NA_T * e;
     if (NA_T * e >= n) break;  // uniform
     const bool live = i < n;
-    const float nv = live ? sr[i] + dv[e] * inv * w[i] : 0.f;
+    const float nv = live ? sv[e] + dv[e] * inv * wv_[e] : 0.f;
     if (live) sr[i] = nv;
-    if (q.d0) qx_store(q, i, live ? nv * next_w[i] : 0.f, nv, live);
+    if (q.d0) qx_store(q, i, live ? nv * nw[e] : 0.f, nv, live);
   }
 }
 
@@ -181,6 +187,91 @@ __global__ __launch_bounds__(256) void k_rope(float *x, const float *w, uint32_t
   }
   if (mode == 0)
     for (uint32_t i = rot + lane; i < hd; i += 64) v[i] = v[i] * w[i] * inv;
+}
+
+// RoPE rotations of a batch of positions: cs[t * rot/2 + i] = (cos, sin) of
+// (start + t) * scale * theta^(-2i/rot), formed in f64 as in k_rope and rounded to f32 once.
+__global__ __launch_bounds__(256) void k_rope_table(float2 *cs, uint32_t half, uint32_t rot, uint32_t n,
+                                                    uint32_t start, const int32_t *start_dev, float theta, float scale) {
+  const uint32_t j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n * half) return;
+  const uint32_t t = j / half, i = j % half;
+  const uint32_t s0 = start_dev ? (uint32_t)*start_dev : start;
+  const double pos = (double)(s0 + t) * (double)scale;
+  const double angle = pos * pow((double)theta, -(double)(2 * i) / (double)rot);
+  double sn, c;
+  sincos(angle, &sn, &c);
+  cs[j] = make_float2((float)c, (float)sn);
+}
+
+hipError_t rope_table(hipStream_t s, float2 *cs, uint32_t rot, uint32_t n, uint32_t start, const int32_t *start_dev,
+                      float theta, float scale) {
+  if (!n) return hipSuccess;
+  if (!rot || rot % 2) return hipErrorInvalidValue;
+  const uint32_t count = n * (rot / 2);
+  hipLaunchKernelGGL(k_rope_table, dim3((count + 255) / 256), dim3(256), 0, s, cs, rot / 2, rot, n, start, start_dev,
+                     theta, scale);
+  return hipGetLastError();
+}
+
+// The finish of the grouped Q/K/V prompt GEMM: per (token, head) one wavefront sums the
+// head's split-K partials in split order, adds the bias, applies k_rope's norm and rotation
+// (rotations from rope_table, the same f64 angles) to Q and K heads, and writes Q to q and K / V straight into the
+// ring slot of the token's position (k_kv_append's slot). The head is staged in LDS so any
+// rotary width and pair layout can be read back.
+__global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
+  __shared__ float buf[4][512];
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t per = a.heads + 2 * a.kvh, hd = a.hd;
+  const uint32_t item = blockIdx.x * 4 + wv;
+  if (item >= a.batch * per) return;
+  const uint32_t tok = item / per, slot = item % per;
+  const int kind = slot < a.heads ? 0 : slot < a.heads + a.kvh ? 1 : 2;
+  const uint32_t h = kind == 0 ? slot : kind == 1 ? slot - a.heads : slot - a.heads - a.kvh;
+  const float *bias = kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv;
+  const uint64_t n = (uint64_t)a.rows_total * a.batch, base = (uint64_t)tok * a.rows_total + (uint64_t)slot * hd;
+  float *v = buf[wv];
+  for (uint32_t d = lane; d < hd; d += 64) {
+    float acc = 0.f;
+    for (uint32_t z = 0; z < a.splits; z++) acc += a.part[z * n + base + d];
+    v[d] = bias ? acc + bias[h * hd + d] : acc;
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t s0 = a.start_dev ? (uint32_t)*a.start_dev : a.start;
+  const uint64_t ring = (uint64_t)((s0 + tok) % a.capacity) * a.kvh * hd + (uint64_t)h * hd;
+  float *dst = kind == 0 ? a.q + ((uint64_t)tok * a.heads + h) * hd : kind == 1 ? a.kc + ring : a.vc + ring;
+  if (kind == 2) {
+    for (uint32_t d = lane; d < hd; d += 64) dst[d] = v[d];
+    return;
+  }
+  const float *w = kind == 0 ? a.qn : a.kn;
+  float inv = 1.f;
+  if (a.mode == 0) {
+    float ss = 0.f;
+    for (uint32_t d = lane; d < hd; d += 64) ss += v[d] * v[d];
+    ss = wave_sum(ss);
+    inv = 1.f / sqrtf(ss / (float)hd + a.eps);
+  }
+  const uint32_t half = a.rot / 2;
+  for (uint32_t i = lane; i < half; i += 64) {
+    const float2 t = a.cs[(uint64_t)tok * half + i];
+    const float c = t.x, sf = t.y;
+    const uint32_t ia = a.mode == 2 ? 2 * i : i, ib = a.mode == 2 ? 2 * i + 1 : i + half;
+    float x0 = v[ia], x1 = v[ib];
+    if (a.mode == 0) { x0 = x0 * w[ia] * inv; x1 = x1 * w[ib] * inv; }
+    dst[ia] = x0 * c - x1 * sf;
+    dst[ib] = x0 * sf + x1 * c;
+  }
+  for (uint32_t d = a.rot + lane; d < hd; d += 64) dst[d] = a.mode == 0 ? v[d] * w[d] * inv : v[d];
+}
+
+hipError_t qkv_finish(hipStream_t s, const QKVFinish &a) {
+  if (!a.batch) return hipSuccess;
+  if (a.hd > 512 || a.rot > a.hd || a.rot % 2 || !a.capacity || !a.cs || (a.mode == 0 && (!a.qn || !a.kn)))
+    return hipErrorInvalidValue;
+  const uint32_t items = a.batch * (a.heads + 2 * a.kvh);
+  hipLaunchKernelGGL(k_qkv_finish, dim3((items + 3) / 4), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 hipError_t rope(hipStream_t s, float *x, const float *w, uint32_t heads, uint32_t hd, uint32_t start,
