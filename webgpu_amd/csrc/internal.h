@@ -116,6 +116,10 @@ hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *i
                  uint32_t hidden, uint32_t n, double scale);
 hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_t n, float eps,
                 uint32_t batch);
+// Per token: state += the split-K partial sums part[z][tok][n] (in split order), then
+// norm_split() of the new state into y and xs (n % 64 == 0, n <= 16384).
+hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
+                             uint16_t *xs, uint32_t n, float eps, uint32_t batch);
 // norm() that also writes its output in the prompt GEMM's split form into xs (n % 64 == 0).
 hipError_t norm_split(hipStream_t s, const float *x, const float *w, float *y, uint16_t *xs, uint32_t n, float eps,
                       uint32_t batch);

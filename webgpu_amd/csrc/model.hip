@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
+#include <utility>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -188,6 +189,14 @@ static GemmGroup glu_group(wgd_model *m, const Layer &L) {
   return g;
 }
 
+// A residual projection kept as split-K partials for the fused norm finish.
+static GemmGroup res_group(wgd_model *m, const Matrix &W) {
+  GemmGroup g;
+  g.job[0] = GemmJob{&W, m->hidden, (uint32_t)m->c.hidden, 0};
+  g.n = 1; g.keep_partials = true;
+  return g;
+}
+
 // n tokens already gathered into m->hidden (a prompt chunk, or one decode token on the
 // generic path with its position in device memory).
 hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_t *start_dev = nullptr) {
@@ -220,9 +229,33 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       WGD_HIP(rope_table(s, m->rope_batch[1], c.head_dim, n, start, start_dev, r1.theta, r1.scale));
     }
   }
+  // A residual projection (O, down) into m->hidden: with the next RMSNorm fused into its
+  // split-K finish when that norm feeds a split-input GEMM (then returns true: m->normed and
+  // its split are ready), else added by the GEMM's own reduction, else the generic path.
+  auto residual = [&](const Matrix &W, const float *x, const float *bias_w, const float *post_w,
+                      const float *next_w, const Matrix *next_first) -> std::pair<hipError_t, bool> {
+    if (!gemma && !bias_w && gemm_splits_input(W, &gs, n)) {
+      if (next_w && next_first && gemm_splits_input(*next_first, &gs, n) && H <= 16384) {
+        GemmGroup g = res_group(m, W);
+        uint32_t splits = 0;
+        g.splits = &splits;
+        hipError_t e = gemm_group(s, g, x, n, &gs);
+        if (e == hipSuccess) e = reduce_norm_split(s, gs.p, splits, m->hidden, next_w, m->normed, gs.xs, H, c.epsilon, n);
+        gs.xs_of = m->normed; gs.xs_cols = H; gs.xs_batch = n;
+        return {e, true};
+      }
+      return {matmul(s, W, x, m->hidden, H, 0, 0, n, &gs, true), false};
+    }
+    hipError_t e = matmul(s, W, x, m->proj, H, 0, 0, n, &gs);
+    if (e == hipSuccess) e = bias(s, m->proj, bias_w, n, H);
+    if (e == hipSuccess) e = gemma ? norm_add(s, m->proj, post_w, m->hidden, H, c.epsilon, n) : add(s, m->proj, m->hidden, n * H);
+    return {e, false};
+  };
+  bool normed_ready = false;  // m->normed (and its split) already hold this layer's attention-norm input
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
-    WGD_HIP(norm_for(L.attn_norm, L.q));
+    if (!normed_ready) WGD_HIP(norm_for(L.attn_norm, L.q));
+    normed_ready = false;
     GemmGroup qkv = qkv_group(m, L);
     uint32_t splits = 0;
     qkv.keep_partials = true; qkv.splits = &splits;
@@ -251,15 +284,9 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       WGD_HIP(attention_block(m, l, n, start, start_dev));
     }
     gs.xs_of = nullptr;
-    if (!gemma && !L.bo && gemm_splits_input(L.o, &gs, n)) {
-      WGD_HIP(matmul(s, L.o, m->att, m->hidden, H, 0, 0, n, &gs, true));
-    } else {
-      WGD_HIP(matmul(s, L.o, m->att, m->proj, H, 0, 0, n, &gs));
-      WGD_HIP(bias(s, m->proj, L.bo, n, H));
-      if (gemma) WGD_HIP(norm_add(s, m->proj, L.post_attn, m->hidden, H, c.epsilon, n));
-      else WGD_HIP(add(s, m->proj, m->hidden, n * H));
-    }
-    WGD_HIP(norm_for(L.ffn_norm, L.up));
+    auto ro = residual(L.o, m->att, L.bo, L.post_attn, L.ffn_norm, &L.up);
+    WGD_HIP(ro.first);
+    if (!ro.second) WGD_HIP(norm_for(L.ffn_norm, L.up));
     float *ffn_in = m->up;
     const GemmGroup gu = glu_group(m, L);
     if (c.ffn_gate && gemm_splits_input(L.up, &gs, n) && gemm_group_ok(gu, n)) {
@@ -281,13 +308,11 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       WGD_HIP(activate(s, m->up, n * F));
       gs.xs_of = nullptr;
     }
-    if (!gemma && gemm_splits_input(L.down, &gs, n)) {
-      WGD_HIP(matmul(s, L.down, ffn_in, m->hidden, H, 0, 0, n, &gs, true));
-    } else {
-      WGD_HIP(matmul(s, L.down, ffn_in, m->down, H, 0, 0, n, &gs));
-      if (gemma) WGD_HIP(norm_add(s, m->down, L.post_ffw, m->hidden, H, c.epsilon, n));
-      else WGD_HIP(add(s, m->down, m->hidden, n * H));
-    }
+    const bool last = l + 1 == c.layers;
+    auto rd = residual(L.down, ffn_in, nullptr, L.post_ffw, last ? nullptr : m->L[l + 1].attn_norm,
+                       last ? nullptr : &m->L[l + 1].q);
+    WGD_HIP(rd.first);
+    normed_ready = rd.second;
   }
   return hipSuccess;
 }
@@ -686,6 +711,8 @@ int wgd_model_ready(wgd_model *m) {
         gx = std::max(gx, gemm_input_elems(w->cols, (uint32_t)c.batch));
       }
     gp = std::max(gp, gemm_group_split_floats(qkv_group(m, L), (uint32_t)c.batch));
+    if (L.o.data) gp = std::max(gp, gemm_group_split_floats(res_group(m, L.o), (uint32_t)c.batch));
+    if (L.down.data) gp = std::max(gp, gemm_group_split_floats(res_group(m, L.down), (uint32_t)c.batch));
     if (c.ffn_gate) gp = std::max(gp, gemm_group_split_floats(glu_group(m, L), (uint32_t)c.batch));
   }
   if (gp && !m->gemm_part.p) {

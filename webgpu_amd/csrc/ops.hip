@@ -68,6 +68,72 @@ __global__ __launch_bounds__(256) void k_norm_split(const float *x, const float 
   }
 }
 
+// The finish of a residual projection (O or down) kept as split-K partials, fused with the
+// RMSNorm that reads the residual next: per token, state += the partials summed in split
+// order, then y = RMSNorm(state) * w and its split form xs. One 512-thread workgroup per
+// token, eight consecutive elements per thread step (n <= RN_G * 8 * 512).
+constexpr uint32_t RN_T = 512, RN_G = 4;
+__global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, uint32_t splits, float *state,
+                                                           const float *w, float *y, uint16_t *xs, uint32_t n,
+                                                           uint32_t batch, float eps) {
+  __shared__ float red[RN_T / 64];
+  const uint32_t tok = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t stride = (uint64_t)n * batch;
+  float *sr = state + (uint64_t)tok * n;
+  float v[RN_G][8];
+  float ss = 0.f;
+#pragma unroll
+  for (uint32_t gi = 0; gi < RN_G; gi++) {
+    const uint32_t k = 8 * (tid + RN_T * gi);
+    if (k >= n) break;  // uniform per thread
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    const float *p = part + (uint64_t)tok * n + k;
+    for (uint32_t z = 0; z < splits; z++) {
+      const float4 pa = *(const float4 *)(p + z * stride), pb = *(const float4 *)(p + z * stride + 4);
+      a.x += pa.x; a.y += pa.y; a.z += pa.z; a.w += pa.w;
+      b.x += pb.x; b.y += pb.y; b.z += pb.z; b.w += pb.w;
+    }
+    const float4 ha = *(const float4 *)(sr + k), hb = *(const float4 *)(sr + k + 4);
+    a = make_float4(ha.x + a.x, ha.y + a.y, ha.z + a.z, ha.w + a.w);
+    b = make_float4(hb.x + b.x, hb.y + b.y, hb.z + b.z, hb.w + b.w);
+    *(float4 *)(sr + k) = a;
+    *(float4 *)(sr + k + 4) = b;
+    v[gi][0] = a.x; v[gi][1] = a.y; v[gi][2] = a.z; v[gi][3] = a.w;
+    v[gi][4] = b.x; v[gi][5] = b.y; v[gi][6] = b.z; v[gi][7] = b.w;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += v[gi][e] * v[gi][e];
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (uint32_t u = 0; u < RN_T / 64; u++) ss += red[u];
+  const float inv = 1.f / sqrtf(ss / (float)n + eps);
+  float *yr = y + (uint64_t)tok * n;
+#pragma unroll
+  for (uint32_t gi = 0; gi < RN_G; gi++) {
+    const uint32_t k = 8 * (tid + RN_T * gi);
+    if (k >= n) break;
+    const float4 wa = *(const float4 *)(w + k), wb = *(const float4 *)(w + k + 4);
+    const float4 a = make_float4(v[gi][0] * inv * wa.x, v[gi][1] * inv * wa.y, v[gi][2] * inv * wa.z, v[gi][3] * inv * wa.w);
+    const float4 b = make_float4(v[gi][4] * inv * wb.x, v[gi][5] * inv * wb.y, v[gi][6] * inv * wb.z, v[gi][7] * inv * wb.w);
+    *(float4 *)(yr + k) = a;
+    *(float4 *)(yr + k + 4) = b;
+    split_store8(xs, n, tok, k, a, b);
+  }
+}
+
+hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
+                             uint16_t *xs, uint32_t n, float eps, uint32_t batch) {
+  if (!batch) return hipSuccess;
+  if (n % SPLIT_K || n > RN_G * 8 * RN_T || !splits ||
+      ((uintptr_t)part | (uintptr_t)state | (uintptr_t)w | (uintptr_t)y) % 16)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_reduce_norm_split, dim3(batch), dim3(RN_T), 0, s, part, splits, state, w, y, xs, n, batch, eps);
+  return hipGetLastError();
+}
+
 hipError_t norm_split(hipStream_t s, const float *x, const float *w, float *y, uint16_t *xs, uint32_t n, float eps,
                       uint32_t batch) {
   if (!batch) return hipSuccess;
