@@ -14,6 +14,7 @@
 #include "internal.h"
 #include "decode.h"
 #include "attention.h"
+#include "split.h"
 
 namespace wgd {
 
@@ -143,8 +144,11 @@ __global__ __launch_bounds__(256) void k_attention(AttnK a) {
   }
 }
 
+// With xs set (hd % 8 == 0, heads * hd % 64 == 0), the output row is also written in the
+// prompt GEMM's split form for the O projection (row = token * heads + head).
 __global__ __launch_bounds__(128) void k_attention_combine(const float *part, float *y, uint32_t rows,
-                                                           uint32_t hd, uint32_t nsplit) {
+                                                           uint32_t hd, uint32_t nsplit, uint16_t *xs, uint32_t heads) {
+  __shared__ float out[512];
   const uint64_t row = blockIdx.x;
   const uint64_t stride = (uint64_t)rows * (hd + 2);
   float M = -INFINITY;
@@ -160,8 +164,16 @@ __global__ __launch_bounds__(128) void k_attention_combine(const float *part, fl
       const float *pp = part + z * stride + row * (hd + 2);
       if (pp[0] != -INFINITY) acc += pp[2 + d] * expf(pp[0] - M);
     }
-    y[row * hd + d] = L > 0.f ? acc / L : 0.f;
+    const float o = L > 0.f ? acc / L : 0.f;
+    y[row * hd + d] = o;
+    out[d] = o;
   }
+  if (!xs) return;
+  __syncthreads();
+  const uint32_t tok = (uint32_t)(row / heads), h = (uint32_t)(row % heads);
+  for (uint32_t g = threadIdx.x; g < hd / 8; g += blockDim.x)
+    split_store8(xs, heads * hd, tok, h * hd + 8 * g, make_float4(out[8 * g], out[8 * g + 1], out[8 * g + 2], out[8 * g + 3]),
+                 make_float4(out[8 * g + 4], out[8 * g + 5], out[8 * g + 6], out[8 * g + 7]));
 }
 
 // Prompt batches on the f32 matrix cores (v_mfma_f32_16x16x4_f32: f32 products, f32 sums, as
@@ -333,9 +345,11 @@ static hipError_t launch_attn_prompt(hipStream_t s, AttnK a, const AttnArgs &in,
   hipLaunchKernelGGL(k_attn_prompt<HD>, dim3(in.kv_heads, (nqt * a.group + 3) / 4, nsplit), dim3(256), lds, s, a);
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
+    uint16_t *xs = in.xs && in.hd % 8 == 0 && in.heads * in.hd % 64 == 0 ? in.xs : nullptr;
     hipLaunchKernelGGL(k_attention_combine, dim3(in.batch * in.heads), dim3(128), 0, s, (const float *)in.partial,
-                       in.y, in.batch * in.heads, in.hd, nsplit);
+                       in.y, in.batch * in.heads, in.hd, nsplit, xs, in.heads);
     WGD_HIP(hipGetLastError());
+    if (in.xs_written) *in.xs_written = xs != nullptr;
   }
   return hipSuccess;
 }
@@ -401,7 +415,7 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
     hipLaunchKernelGGL(k_attention_combine, dim3(in.batch * in.heads), dim3(128), 0, s, (const float *)in.partial,
-                       in.y, in.batch * in.heads, in.hd, nsplit);
+                       in.y, in.batch * in.heads, in.hd, nsplit, (uint16_t *)nullptr, in.heads);
     WGD_HIP(hipGetLastError());
   }
   return hipSuccess;

@@ -148,6 +148,8 @@ struct AttnArgs {
   uint32_t heads, kv_heads, hd, start; const int32_t *start_dev;
   float scale; uint32_t window, capacity, batch;
   float *partial; uint32_t partial_floats;  // split-K scratch (may be null: single split)
+  // optional: the output also in the prompt GEMM's split form; *xs_written says whether it was
+  uint16_t *xs = nullptr; bool *xs_written = nullptr;
 };
 hipError_t attention(hipStream_t s, const AttnArgs &a);
 uint64_t attention_scratch_floats(uint32_t heads, uint32_t hd, uint32_t batch, uint32_t max_keys);

@@ -125,7 +125,7 @@ static RopeParams rope_params(wgd_model *m, int l) {
 // Attention of one layer, with RoPE and the KV append unless `prepared` (the Q/K/V GEMM
 // finish did them); positions from start (host) or start_dev.
 hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, const int32_t *start_dev,
-                           bool prepared = false) {
+                           bool prepared = false, uint16_t *xs = nullptr, bool *xs_written = nullptr) {
   const wgd_model_config &c = m->c;
   Layer &L = m->L[l];
   hipStream_t s = m->ctx->stream;
@@ -142,6 +142,7 @@ hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, cons
   a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = hd; a.start = start; a.start_dev = start_dev;
   a.scale = c.attention_scale; a.window = window_of(m, l); a.capacity = L.cap; a.batch = n;
   a.partial = m->att_part; a.partial_floats = (uint32_t)m->att_part_floats;
+  a.xs = xs; a.xs_written = xs_written;
   return attention(s, a);
 }
 
@@ -273,7 +274,11 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       f.eps = r.eps; f.mode = r.mode;
       f.cs = m->rope_batch[gemma && local_layer(m, l) ? 1 : 0];
       WGD_HIP(qkv_finish(s, f));
-      WGD_HIP(attention_block(m, l, n, start, start_dev, true));
+      // the attention output's split for the O GEMM comes from the key-split merge
+      bool written = false;
+      const bool want = gemm_splits_input(L.o, &gs, n);
+      WGD_HIP(attention_block(m, l, n, start, start_dev, true, want ? gs.xs : nullptr, &written));
+      gs.xs_of = written ? m->att : nullptr; gs.xs_cols = qd; gs.xs_batch = n;
     } else {
       WGD_HIP(matmul(s, L.q, m->normed, m->q, qd, 0, 0, n, &gs));
       WGD_HIP(matmul(s, L.k, m->normed, m->k, kd, 0, 0, n, &gs));
@@ -282,8 +287,8 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       WGD_HIP(bias(s, m->k, L.bk, n, kd));
       WGD_HIP(bias(s, m->v, L.bv, n, kd));
       WGD_HIP(attention_block(m, l, n, start, start_dev));
+      gs.xs_of = nullptr;
     }
-    gs.xs_of = nullptr;
     auto ro = residual(L.o, m->att, L.bo, L.post_attn, L.ffn_norm, &L.up);
     WGD_HIP(ro.first);
     if (!ro.second) WGD_HIP(norm_for(L.ffn_norm, L.up));
