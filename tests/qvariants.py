@@ -1,0 +1,95 @@
+"""Small quantized GGUF variants for the GPU parity tests: the planar-weight prompt path
+(grouped GEMMs and their fused finishes) and the quantized decode path under model features
+the three shaped decoders do not use.
+
+* ``qwen2-bias``: Q/K/V biases, half-split RoPE, SwiGLU (gguf.ts:168-170 detects the bias).
+* ``llama-partial``: adjacent-pair RoPE over 32 of 64 dims, Q/K/V and output biases, an
+  ungated FFN (SiLU of up), a sliding window.
+* ``qwen3-mixed``: Q/K norm, partial rotary with linear RoPE scaling, and a Q8_0 K
+  projection beside Q4_K Q and Q6_K V (three weight types: the Q/K/V group falls back to
+  one launch per matrix).
+
+Dimensions are the smallest the planar K-quant kernels take: hidden 256 (Q4_K/Q6_K rows of
+whole 256-element blocks), 4 query heads x 64, 2 KV heads, FFN 512, vocab 300. Matrix blocks
+come from the synthetic generators (webgpu_amd/synth.py); norm and bias vectors are f32.
+"""
+from typing import List, Tuple
+
+import numpy as np
+
+from webgpu_amd import synth
+from webgpu_amd.gguf import F32, Q4_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
+
+KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed")
+
+
+def build(kind: str):
+    """(file bytes, parsed header, model config) of variant ``kind``."""
+    rng = np.random.default_rng(sum(kind.encode()) * 31 + 5)
+    H, nh, nkv, hd, F, V, L = 256, 4, 2, 64, 512, 300, 2
+    arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3"}[kind]
+    qd, kd = nh * hd, nkv * hd
+    T: List[Tuple[str, List[int], int, np.ndarray]] = []
+
+    def mat(name, cols, rows, typ, std=0.05):
+        nb = rows * cols // QUANTS[typ]["block"]
+        gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[typ]
+        T.append((name, [cols, rows], typ, gen(rng, nb, std)))
+
+    def vec(name, n, center=1.0, spread=0.1):
+        v = (center + rng.uniform(-spread, spread, n)).astype(np.float32)
+        T.append((name, [n], F32, v.view(np.uint8)))
+
+    mat("token_embd.weight", H, V, Q6_K, 0.5)
+    vec("output_norm.weight", H)
+    mat("output.weight", H, V, Q6_K, 0.3)
+    k_type = Q8_0 if kind == "qwen3-mixed" else Q4_K
+    for l in range(L):
+        p = f"blk.{l}."
+        vec(p + "attn_norm.weight", H)
+        mat(p + "attn_q.weight", H, qd, Q4_K)
+        mat(p + "attn_k.weight", H, kd, k_type)
+        mat(p + "attn_v.weight", H, kd, Q6_K)
+        mat(p + "attn_output.weight", qd, H, Q4_K)
+        if kind in ("qwen2-bias", "llama-partial"):
+            vec(p + "attn_q.bias", qd, 0.0, 0.2)
+            vec(p + "attn_k.bias", kd, 0.0, 0.2)
+            vec(p + "attn_v.bias", kd, 0.0, 0.2)
+        if kind == "llama-partial":
+            vec(p + "attn_output.bias", H, 0.0, 0.1)
+        if kind == "qwen3-mixed":
+            vec(p + "attn_q_norm.weight", hd)
+            vec(p + "attn_k_norm.weight", hd)
+        vec(p + "ffn_norm.weight", H)
+        if kind != "llama-partial":
+            mat(p + "ffn_gate.weight", H, F, Q4_K)
+        mat(p + "ffn_up.weight", H, F, Q4_K)
+        mat(p + "ffn_down.weight", F, H, Q4_K)
+    meta = [("general.architecture", 8, arch), ("general.name", 8, kind),
+            (f"{arch}.block_count", 4, L), (f"{arch}.context_length", 4, 4096),
+            (f"{arch}.embedding_length", 4, H), (f"{arch}.feed_forward_length", 4, F),
+            (f"{arch}.attention.head_count", 4, nh), (f"{arch}.attention.head_count_kv", 4, nkv),
+            (f"{arch}.attention.key_length", 4, hd), (f"{arch}.attention.value_length", 4, hd),
+            (f"{arch}.attention.layer_norm_rms_epsilon", 6, 1e-5)]
+    if kind == "qwen2-bias":
+        meta += [(f"{arch}.rope.freq_base", 6, 1e6), (f"{arch}.rope.dimension_count", 4, hd)]
+    elif kind == "llama-partial":
+        meta += [(f"{arch}.rope.freq_base", 6, 1e4), (f"{arch}.rope.dimension_count", 4, 32),
+                 (f"{arch}.attention.sliding_window", 4, 24)]
+    else:
+        meta += [(f"{arch}.rope.freq_base", 6, 1e6), (f"{arch}.rope.dimension_count", 4, 48),
+                 (f"{arch}.rope.scaling.type", 8, "linear"), (f"{arch}.rope.scaling.factor", 6, 2.0)]
+    entries = [(n, d, t, "") for n, d, t, _ in T]
+    offsets, off = [], 0
+    for _, dims, typ, _ in T:
+        off = -(-off // 32) * 32
+        offsets.append(off)
+        off += synth.tensor_bytes(dims, typ)
+    header = synth._header(meta, entries, offsets)
+    start = -(-len(header) // 32) * 32
+    f = np.zeros(start + -(-off // 32) * 32, np.uint8)
+    f[:len(header)] = np.frombuffer(header, np.uint8)
+    for (_, _, _, data), o in zip(T, offsets):
+        f[start + o:start + o + data.size] = data
+    g = parse_gguf_header(f, f.size)
+    return f, g, model_config(g)
