@@ -19,12 +19,31 @@ import numpy as np
 
 from webgpu_amd import synth
 from webgpu_amd.gguf import F32, Q4_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
+from webgpu_amd.tokenizer import byte_alphabet
 
 KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed")
 
 
-def build(kind: str):
-    """(file bytes, parsed header, model config) of variant ``kind``."""
+CHAT_SPECIALS = ["<|im_start|>", "<|im_end|>", "<|endoftext|>"]
+CHAT_MERGES = ["h e", "he l", "hel l", "hell o", "Ġ w", "Ġw o", "Ġwo r", "Ġwor l", "Ġworl d", "u s", "us e", "use r"]
+
+
+def _tokenizer_meta(vocab: int):
+    """A byte-level BPE vocabulary of ``vocab`` entries with ChatML control tokens: the 256
+    single-byte symbols, a few merges, the specials, then unused fillers."""
+    tokens = [*byte_alphabet(), *["".join(m.split(" ")) for m in CHAT_MERGES], *CHAT_SPECIALS]
+    tokens += [f"<unused{i}>" for i in range(vocab - len(tokens))]
+    types = [1] * (256 + len(CHAT_MERGES)) + [3] * (vocab - 256 - len(CHAT_MERGES))
+    return [("tokenizer.ggml.model", 8, "gpt2"), ("tokenizer.ggml.pre", 8, "qwen2"),
+            ("tokenizer.ggml.tokens", 9, (8, tokens)), ("tokenizer.ggml.merges", 9, (8, CHAT_MERGES)),
+            ("tokenizer.ggml.token_type", 9, (5, types)),
+            ("tokenizer.ggml.eos_token_id", 4, tokens.index("<|im_end|>")),
+            ("tokenizer.chat_template", 8, "{% for m in messages %}<|im_start|>{{ m.role }}\n{{ m.content }}<|im_end|>\n{% endfor %}")]
+
+
+def build(kind: str, tokenizer: bool = False):
+    """(file bytes, parsed header, model config) of variant ``kind``; with ``tokenizer`` the
+    file also carries a byte-level BPE vocabulary with a ChatML template."""
     rng = np.random.default_rng(sum(kind.encode()) * 31 + 5)
     H, nh, nkv, hd, F, V, L = 256, 4, 2, 64, 512, 300, 2
     arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3"}[kind]
@@ -79,6 +98,8 @@ def build(kind: str):
     else:
         meta += [(f"{arch}.rope.freq_base", 6, 1e6), (f"{arch}.rope.dimension_count", 4, 48),
                  (f"{arch}.rope.scaling.type", 8, "linear"), (f"{arch}.rope.scaling.factor", 6, 2.0)]
+    if tokenizer:
+        meta += _tokenizer_meta(V)
     entries = [(n, d, t, "") for n, d, t, _ in T]
     offsets, off = [], 0
     for _, dims, typ, _ in T:

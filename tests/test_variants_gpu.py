@@ -76,3 +76,34 @@ def test_quantized_variant_graph_decode_matches_eager(kind):
         assert dev == eager
     finally:
         eng.dispose()
+
+
+def test_generate_from_chat_messages():
+    # the text front-end end to end: the GGUF's own byte-level BPE vocabulary and ChatML
+    # framing turn messages into the prompt; the greedy continuation equals the oracle's
+    # on the same ids, and each event's text is the decode of the tokens so far
+    from webgpu_amd.engine import GenerationOptions
+    f, g, c = qvariants.build("qwen2-bias", tokenizer=True)
+    eng = PagedEngine()
+    eng.load(f, LoadOptions(contextLength=256, batchSize=64))
+    ora = orc.OracleModel(f, g, c, 256, attention_memory(c, 256, 64)["capacities"])
+    try:
+        tok = eng.tokenizer
+        assert tok is not None and tok.style == "chatml"
+        messages = [{"role": "user", "content": "hello world, user"}]
+        ids = tok.chat(messages)
+        events = list(eng.generate(messages, GenerationOptions(maxTokens=8)))
+        want, logits, pos = [], ora.forward(ids, 0), len(ids)
+        for _ in range(8):
+            t = int(np.argmax(logits))
+            if t in tok.eos:
+                break
+            want.append(t)
+            logits = ora.forward([t], pos)
+            pos += 1
+        assert [e.token for e in events] == want
+        for i, e in enumerate(events):
+            assert e.text == tok.decode(want[:i + 1]) and e.promptTokens == len(ids)
+    finally:
+        ora.close()
+        eng.dispose()

@@ -6,9 +6,10 @@ greedy ``sample``. GGUF parsing, configuration and KV-ring sizing run on the hos
 as in gguf.ts/context.ts; weights are uploaded once and stay resident (the pager of
 pager.ts collapses), and each forward / decode step runs inside libwgd on the GPU.
 
-Tokenizers are not part of this runtime: ``generate`` takes prompt token ids, or any
-object with ``chat(messages) -> ids``, ``decode(ids) -> str`` and ``eos`` (the shape of
-the reference's tokenizers) passed as ``tokenizer``.
+``generate`` takes chat messages (``[{"role": "user", "content": ...}]``), framed by the
+GGUF's own tokenizer (tokenizer.py, picked as engine.ts:67-69 does), or prompt token ids.
+A ``tokenizer`` argument (any object with ``chat``, ``decode`` and ``eos``) overrides the
+model's.
 """
 from __future__ import annotations
 
@@ -22,9 +23,10 @@ from typing import Any, Dict, Iterator, List, Optional, Sequence
 
 import numpy as np
 
-from .context import MAX_CONTEXT, attention_memory, output_limit, validate_context
+from .context import MAX_CONTEXT, MAX_MESSAGE_CHARS, attention_memory, output_limit, validate_context
 from .gguf import GGUF, ModelConfig, Tensor, model_config, read_gguf
 from .gpu import Compute, ModelConfigC, WgdError, lib
+from .tokenizer import tokenizer_for
 
 BATCHES = (1, 8, 16, 32, 64, 128)
 
@@ -137,6 +139,7 @@ class PagedEngine:
         self.busy = False
         self.disposed = False
         self.tokensInCache: List[int] = []
+        self.tokenizer = None
 
     # ------------------------------------------------------------------ load
     def load(self, source, options: Optional[LoadOptions] = None) -> ModelInfo:
@@ -153,6 +156,8 @@ class PagedEngine:
         self.gguf = read_gguf(self.source)
         self.config = c = model_config(self.gguf)
         validate_context(self.context, c.maxContext)
+        # the GGUF's tokenizer (None for a file that carries none: token-id prompts only)
+        self.tokenizer = tokenizer_for(self.gguf.metadata, c.architecture, c.family)
         memory = attention_memory(c, self.context, self.batch)
         self.kvCapacities = list(memory["capacities"])
         self.gpu = Compute(o.gpuBudgetMiB, o.device)
@@ -232,7 +237,18 @@ class PagedEngine:
             raise ValueError(f"maxTokens must be 1–{MAX_CONTEXT}.")
         if o.temperature != 0:
             raise ValueError("Only greedy decoding (temperature 0) is implemented by this runtime.")
-        ids = list(tokenizer.chat(prompt)) if tokenizer is not None else [int(t) for t in prompt]
+        tokenizer = tokenizer if tokenizer is not None else self.tokenizer
+        messages = isinstance(prompt, (list, tuple)) and len(prompt) > 0 and all(isinstance(m, dict) for m in prompt)
+        if messages:
+            # engine.ts:260: user/assistant text messages of bounded length
+            if any(m.get("role") not in ("user", "assistant") or not isinstance(m.get("content"), str) or
+                   len(m["content"]) > MAX_MESSAGE_CHARS for m in prompt):
+                raise ValueError(f"Provide user/assistant text messages (at most {MAX_MESSAGE_CHARS:,} characters each).")
+            if tokenizer is None:
+                raise ValueError("This model carries no tokenizer: pass prompt token ids.")
+            ids = list(tokenizer.chat(prompt))
+        else:
+            ids = [int(t) for t in prompt]
         if not ids:
             raise ValueError("Provide a non-empty prompt.")
         eos = set(getattr(tokenizer, "eos", ()) or ())

@@ -193,17 +193,30 @@ def _header(meta, tensors, offsets) -> bytes:
     def s(v: str) -> None:
         b = v.encode()
         out.extend(struct.pack("<Q", len(b)) + b)
-    for key, typ, val in meta:
-        s(key)
-        out.extend(struct.pack("<I", typ))
+
+    def scalar(typ: int, val) -> None:
         if typ == 8:
             s(val)
         elif typ == 4:
             out.extend(struct.pack("<I", val))
+        elif typ == 5:
+            out.extend(struct.pack("<i", val))
         elif typ == 6:
             out.extend(struct.pack("<f", val))
+        elif typ == 7:
+            out.extend(struct.pack("<B", 1 if val else 0))
         else:
             raise ValueError(typ)
+    for key, typ, val in meta:
+        s(key)
+        out.extend(struct.pack("<I", typ))
+        if typ == 9:  # array: (element type, values)
+            et, vals = val
+            out.extend(struct.pack("<IQ", et, len(vals)))
+            for v in vals:
+                scalar(et, v)
+        else:
+            scalar(typ, val)
     for (name, dims, typ, _), off in zip(tensors, offsets):
         s(name)
         out.extend(struct.pack("<I", len(dims)))
