@@ -211,6 +211,78 @@ def test_token_loop_runs_to_the_exact_context_boundary():
     assert not eng.busy
 
 
+def _scripted_engine(context, batch, caps):
+    eng = PagedEngine()
+    eng.context, eng.batch, eng.model, eng.kvCapacities = context, batch, object(), caps
+    counts = []
+    eng.forward = lambda ids, start, logits=False: None
+    eng.forward_argmax = lambda ids, start: 7
+
+    def decode(token, start, count):
+        counts.append(count)
+        return [7] * count
+    eng.decode = decode
+    eng.stats = lambda: {}
+    return eng, counts
+
+
+def test_device_chunks_stay_within_the_sliding_ring_slack():
+    # a ring of window + batch - 1 slots survives at most `batch` positions written past
+    # the cached prefix, so a model with one decodes at most `batch` tokens per chunk
+    eng, counts = _scripted_engine(256, 8, [31, 256])
+    assert len(list(eng.generate([1, 2, 3], GenerationOptions(maxTokens=100)))) == 100
+    assert max(counts) == 8
+    eng, counts = _scripted_engine(256, 8, [256, 256])
+    list(eng.generate([1, 2, 3], GenerationOptions(maxTokens=100)))
+    assert max(counts) == 32
+
+
+def test_abort_signal_stops_generation_and_drops_the_prefix():
+    from webgpu_amd.engine import AbortError, AbortSignal
+    eng, _ = _scripted_engine(512, 16, [512])
+    sig = AbortSignal()
+    got = []
+    with pytest.raises(AbortError, match="Stopped by user"):
+        for ev in eng.generate([1, 2, 3], GenerationOptions(maxTokens=50), signal=sig):
+            got.append(ev.token)
+            if len(got) == 3:
+                sig.abort()
+    assert len(got) == 3 and eng.tokensInCache == [] and not eng.busy
+
+
+def test_generation_options_are_validated_like_the_reference():
+    eng, _ = _scripted_engine(512, 16, [512])
+    for bad in (dict(temperature=-1), dict(temperature=2.5), dict(topK=0), dict(topK=201),
+                dict(topP=0), dict(topP=1.5), dict(temperature=float("nan"))):
+        with pytest.raises(ValueError, match="Invalid sampling settings"):
+            eng.generate([1], GenerationOptions(**bad))
+    with pytest.raises(ValueError, match="maxTokens"):
+        eng.generate([1], GenerationOptions(maxTokens=0))
+
+
+def test_an_unstarted_generation_leaves_the_engine_free():
+    eng, _ = _scripted_engine(512, 16, [512])
+    eng.generate([1, 2], GenerationOptions(maxTokens=4))   # never iterated
+    assert not eng.busy
+    assert len(list(eng.generate([1, 2], GenerationOptions(maxTokens=4)))) == 4
+
+
+def test_load_options_follow_the_performance_presets():
+    from webgpu_amd.engine import LoadOptions
+    eng = PagedEngine()
+    with pytest.raises(ValueError, match="Performance must be"):
+        eng.load(b"\0" * 64, LoadOptions(performance="turbo"))
+    for mode, batch in (("lite", 8), ("low-memory", 16), ("fast", 128)):
+        eng = PagedEngine()
+        with pytest.raises(ValueError):   # not a GGUF: fails after the options are taken
+            eng.load(b"\0" * 64, LoadOptions(performance=mode))
+        assert eng.batch == batch and eng.performance == mode
+    eng = PagedEngine()
+    with pytest.raises(ValueError):
+        eng.load(b"\0" * 64, LoadOptions(performance="lite", batchSize=64))
+    assert eng.batch == 64
+
+
 def test_generate_rejects_concurrent_and_unloaded_use():
     eng = PagedEngine()
     with pytest.raises(RuntimeError, match="Load a model"):

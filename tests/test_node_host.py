@@ -32,6 +32,18 @@ def run_node(*args, timeout=120):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+@needs_node
+def test_node_generate_rules_without_a_device():
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "engine_rules.mjs")],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr[-3000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["slidingTokens"] == 100 and out["slidingMaxChunk"] == 8 and out["fullMaxChunk"] == 32
+    assert out["abortError"] == "AbortError" and out["abortSeen"] == 3
+    assert out["abortCache"] == 0 and out["abortBusy"] is False
+    assert out["invalid"] == ["Invalid sampling settings."] * 5
+
+
 @pytest.fixture(scope="module")
 def tiny_file(tmp_path_factory):
     f = synth.build("tiny")

@@ -107,3 +107,64 @@ def test_generate_from_chat_messages():
     finally:
         ora.close()
         eng.dispose()
+
+
+def test_sliding_ring_survives_a_turn_that_ends_inside_a_device_chunk():
+    # window 24, batch 8: rings of 31 slots. The first turn ends at an end-of-turn token
+    # early in a device chunk, whose later positions were already written; the second
+    # turn continues the cached prefix and must equal a recompute from scratch.
+    from types import SimpleNamespace
+    from webgpu_amd.engine import GenerationOptions
+    f, g, c = qvariants.build("llama-partial")
+    eng = PagedEngine()
+    eng.load(f, LoadOptions(contextLength=256, batchSize=8))
+    try:
+        assert max(eng.kvCapacities) == 31
+        ids = synth.prompt_ids(c.vocab, 30, seed=21)
+        free = SimpleNamespace(eos=set(), decode=lambda t: "")
+        gen = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=12), tokenizer=free)]
+        stop = gen[2]
+        turn = SimpleNamespace(eos={stop}, decode=lambda t: "")
+        eng.reset()
+        first = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=40), tokenizer=turn)]
+        assert first == gen[:gen.index(stop)]
+        follow = ids + first + [stop, 5, 6, 7, 8]
+        cached = [e.token for e in eng.generate(follow, GenerationOptions(maxTokens=20), tokenizer=free)]
+        eng.reset()
+        fresh = [e.token for e in eng.generate(follow, GenerationOptions(maxTokens=20), tokenizer=free)]
+        assert cached == fresh
+    finally:
+        eng.dispose()
+
+
+def test_runtime_api_drives_the_engine_on_its_worker_thread():
+    # the sdk.ts surface end to end: load, a two-turn chat that reuses the prefix, a
+    # stopped reply, reset, dispose
+    from webgpu_amd.engine import AbortError, GenerationOptions
+    from webgpu_amd.runtime import WebGPU
+    f, g, c = qvariants.build("qwen2-bias", tokenizer=True)
+    rt = WebGPU()
+    ref = PagedEngine()
+    try:
+        info = rt.load(f, LoadOptions(contextLength=256, performance="fast"))
+        assert info.batchSize == 128 and info.performance == "fast" and info.fileBytes == f.size
+        turn1 = [{"role": "user", "content": "hello world"}]
+        a = list(rt.generate(turn1, GenerationOptions(maxTokens=6)))
+        turn2 = turn1 + [{"role": "assistant", "content": a[-1].text if a else ""},
+                         {"role": "user", "content": "hello user"}]
+        b = [e.token for e in rt.generate(turn2, GenerationOptions(maxTokens=6))]
+        ref.load(f, LoadOptions(contextLength=256, batchSize=128))
+        assert [e.token for e in a] == [e.token for e in ref.generate(turn1, GenerationOptions(maxTokens=6))]
+        assert b == [e.token for e in ref.generate(turn2, GenerationOptions(maxTokens=6))]
+        it = rt.generate(turn1, GenerationOptions(maxTokens=200))
+        next(it, None)
+        rt.stop()
+        try:
+            rest, stopped = list(it), False
+        except AbortError:
+            stopped = True
+        assert stopped or len(rest) + 1 < 200   # else the reply had ended at its end-of-turn token
+        rt.reset()
+    finally:
+        rt.dispose()
+        ref.dispose()

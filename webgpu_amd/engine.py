@@ -9,7 +9,10 @@ pager.ts collapses), and each forward / decode step runs inside libwgd on the GP
 ``generate`` takes chat messages (``[{"role": "user", "content": ...}]``), framed by the
 GGUF's own tokenizer (tokenizer.py, picked as engine.ts:67-69 does), or prompt token ids.
 A ``tokenizer`` argument (any object with ``chat``, ``decode`` and ``eos``) overrides the
-model's.
+model's. ``load`` and ``generate`` take an ``AbortSignal`` (the AbortController of
+engine.ts:51,257): an aborted signal stops them at the next weight upload, prompt batch or
+token with ``AbortError``, and a stopped generation drops the cached prefix as the
+reference does (engine.ts:299).
 """
 from __future__ import annotations
 
@@ -17,6 +20,7 @@ import ctypes as C
 import math
 import mmap
 import os
+import threading
 import time
 from dataclasses import dataclass, field
 from typing import Any, Dict, Iterator, List, Optional, Sequence
@@ -29,6 +33,40 @@ from .gpu import Compute, ModelConfigC, WgdError, lib
 from .tokenizer import tokenizer_for
 
 BATCHES = (1, 8, 16, 32, 64, 128)
+# engine.ts:14-18. The prompt batch of each performance mode; the budget and page size of
+# the reference presets belong to its weight pager, which has no counterpart here (every
+# weight is resident).
+PRESETS = {"lite": 8, "low-memory": 16, "fast": 128}
+
+
+class AbortError(RuntimeError):
+    """A load or generation stopped through its ``AbortSignal`` (the DOMException named
+    'AbortError' of worker.ts:9)."""
+
+
+class AbortSignal:
+    """A thread-safe abort flag with the AbortSignal surface the engine uses."""
+
+    def __init__(self) -> None:
+        self._event = threading.Event()
+        self.reason = "Stopped by user"
+
+    @property
+    def aborted(self) -> bool:
+        return self._event.is_set()
+
+    def abort(self, reason: str = "Stopped by user") -> None:
+        self.reason = reason
+        self._event.set()
+
+    def throw_if_aborted(self) -> None:
+        if self._event.is_set():
+            raise AbortError(self.reason)
+
+
+def _check(signal: Optional[AbortSignal]) -> None:
+    if signal is not None:
+        signal.throw_if_aborted()
 
 
 class ByteSource:
@@ -68,16 +106,23 @@ class ByteSource:
 
 @dataclass
 class LoadOptions:
+    """engine.ts:19. ``batchSize`` defaults to the performance mode's batch.
+    ``gpuBudgetMiB`` caps the context's device allocations (None: no cap); the reference's
+    16 GiB ceiling is a browser limit and is not applied."""
     contextLength: int = 512
-    batchSize: int = 128
+    batchSize: Optional[int] = None
     gpuBudgetMiB: Optional[int] = None
+    performance: str = "low-memory"
     device: int = 0
 
 
 @dataclass
 class GenerationOptions:
+    """engine.ts:21, validated as engine.ts:261-264."""
     maxTokens: int = 128
     temperature: float = 0.0
+    topK: int = 40
+    topP: float = 0.9
 
 
 @dataclass
@@ -94,11 +139,14 @@ class TokenEvent:
 
 @dataclass
 class ModelInfo:
+    """engine.ts:23."""
     config: ModelConfig
     fileBytes: int
     adapter: str
     contextLength: int
+    gpuBudgetMiB: Optional[int]
     batchSize: int
+    performance: str
     stats: Dict[str, Any]
 
 
@@ -134,7 +182,9 @@ class PagedEngine:
         self.gguf: Optional[GGUF] = None
         self.config: Optional[ModelConfig] = None
         self.context = 512
-        self.batch = 128
+        self.batch = 16
+        self.budget: Optional[int] = None
+        self.performance = "low-memory"
         self.kvCapacities: List[int] = []
         self.busy = False
         self.disposed = False
@@ -142,15 +192,20 @@ class PagedEngine:
         self.tokenizer = None
 
     # ------------------------------------------------------------------ load
-    def load(self, source, options: Optional[LoadOptions] = None) -> ModelInfo:
+    def load(self, source, options: Optional[LoadOptions] = None, signal: Optional[AbortSignal] = None) -> ModelInfo:
         """PagedEngine.load (engine.ts:51-114): parse, configure, upload, seal."""
         o = options or LoadOptions()
-        self.context, self.batch = o.contextLength, o.batchSize
+        if o.performance not in PRESETS:
+            raise ValueError("Performance must be lite, low-memory or fast.")
+        self.performance = o.performance
+        self.context = o.contextLength
+        self.batch = o.batchSize if o.batchSize is not None else PRESETS[o.performance]
         validate_context(self.context)
         if self.batch not in BATCHES:
             raise ValueError("Batch size must be 1, 8, 16, 32, 64 or 128.")
         if o.gpuBudgetMiB is not None and (not isinstance(o.gpuBudgetMiB, int) or o.gpuBudgetMiB < 512):
             raise ValueError("GPU budget must be at least 512 MiB.")
+        self.budget = o.gpuBudgetMiB
         self.source = source if isinstance(source, ByteSource) else ByteSource(source)
         self.progress({"phase": "loading", "detail": "Reading GGUF metadata", "fraction": 0.05})
         self.gguf = read_gguf(self.source)
@@ -172,6 +227,7 @@ class PagedEngine:
             tensors = [t for t in self.gguf.tensors.values()
                        if len(t.dims) in (1, 2) and (not t.name.startswith("blk.") or int(t.name.split(".")[1]) < c.layers)]
             for i, t in enumerate(tensors):
+                _check(signal)
                 self._upload(t)
                 if i % 64 == 0:
                     self.progress({"phase": "loading", "detail": "Uploading weights", "fraction": 0.1 + 0.85 * i / len(tensors)})
@@ -190,7 +246,7 @@ class PagedEngine:
 
     def info(self) -> ModelInfo:
         return ModelInfo(self.config, self.source.size if self.source else 0, self.gpu.adapterName if self.gpu else "",
-                         self.context, self.batch, self.stats())
+                         self.context, self.budget, self.batch, self.performance, self.stats())
 
     def stats(self) -> Dict[str, Any]:
         return {"gpuBytes": self.gpu.allocated if self.gpu else 0, "peakGpuBytes": self.gpu.peak if self.gpu else 0}
@@ -223,11 +279,16 @@ class PagedEngine:
 
     # ------------------------------------------------------------------ generate
     def generate(self, prompt, options: Optional[GenerationOptions] = None, tokenizer=None,
-                 chunk: int = 32) -> Iterator[TokenEvent]:
+                 chunk: int = 32, signal: Optional[AbortSignal] = None) -> Iterator[TokenEvent]:
         """PagedEngine.generate (engine.ts:257-301) with greedy sampling.
 
         Prefix reuse, output limit, chunked prefill and the busy guard follow the
-        reference; the decode loop runs on the device ``chunk`` tokens at a time."""
+        reference; the decode loop runs on the device ``chunk`` tokens at a time.
+
+        A device chunk may run past an end-of-turn token: its keys land in ring slots
+        beyond the cached prefix. A sliding ring holds the window plus one prompt batch
+        (context.ts:14-23), so at most ``batch`` such positions leave every key the next
+        turn reads in place; the chunk is capped to the batch on models with one."""
         if self.busy:
             raise RuntimeError("A generation is already running.")
         if self.disposed or self.model is None:
@@ -235,7 +296,11 @@ class PagedEngine:
         o = options or GenerationOptions()
         if not isinstance(o.maxTokens, int) or o.maxTokens < 1 or o.maxTokens > MAX_CONTEXT:
             raise ValueError(f"maxTokens must be 1–{MAX_CONTEXT}.")
-        if o.temperature != 0:
+        t, k, p = o.temperature, o.topK, o.topP
+        if (not isinstance(t, (int, float)) or not math.isfinite(t) or t < 0 or t > 2 or not isinstance(k, int)
+                or k < 1 or k > 200 or not isinstance(p, (int, float)) or not math.isfinite(p) or p <= 0 or p > 1):
+            raise ValueError("Invalid sampling settings.")
+        if t != 0:
             raise ValueError("Only greedy decoding (temperature 0) is implemented by this runtime.")
         tokenizer = tokenizer if tokenizer is not None else self.tokenizer
         messages = isinstance(prompt, (list, tuple)) and len(prompt) > 0 and all(isinstance(m, dict) for m in prompt)
@@ -252,10 +317,17 @@ class PagedEngine:
         if not ids:
             raise ValueError("Provide a non-empty prompt.")
         eos = set(getattr(tokenizer, "eos", ()) or ())
-        self.busy = True
-        return self._generate(ids, o, tokenizer, eos, max(1, chunk))
+        chunk = max(1, chunk)
+        if any(cap < self.context for cap in self.kvCapacities):
+            chunk = min(chunk, self.batch)
+        return self._generate(ids, o, tokenizer, eos, chunk, signal)
 
-    def _generate(self, prompt: List[int], o: GenerationOptions, tokenizer, eos, chunk: int) -> Iterator[TokenEvent]:
+    def _generate(self, prompt: List[int], o: GenerationOptions, tokenizer, eos, chunk: int,
+                  signal: Optional[AbortSignal]) -> Iterator[TokenEvent]:
+        # the guard is taken when iteration starts, as for the reference's async generator
+        if self.busy:
+            raise RuntimeError("A generation is already running.")
+        self.busy = True
         try:
             limit = output_limit(o.maxTokens, len(prompt), self.context)
             shared = 0
@@ -268,6 +340,7 @@ class PagedEngine:
             self.tokensInCache = self.tokensInCache[:shared]
             token = -1
             for i in range(shared, len(prompt), self.batch):
+                _check(signal)
                 batch = prompt[i:i + self.batch]
                 last = i + len(batch) == len(prompt)
                 if last:
@@ -279,6 +352,7 @@ class PagedEngine:
             text = ""
             pending: List[int] = []
             for i in range(limit):
+                _check(signal)
                 if not pending and i > 0:
                     count = min(chunk, limit - i)
                     pending = self.decode(token, len(self.tokensInCache), count)

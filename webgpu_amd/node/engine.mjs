@@ -13,6 +13,9 @@ const require = createRequire(import.meta.url);
 const addon = require('./wgd_napi.node');
 
 const BATCHES = [1, 8, 16, 32, 64, 128];
+// engine.ts:14-18: the prompt batch of each performance mode (the budget and page size of
+// the reference presets belong to its weight pager; every weight is resident here).
+export const PRESETS = { lite: 8, 'low-memory': 16, fast: 128 };
 
 /** The wgd_model_config fields for a ModelConfig (field names of include/wgd.h). */
 export function configStruct(c, context, batch, tied) {
@@ -29,18 +32,31 @@ export function configStruct(c, context, batch, tied) {
   };
 }
 
+/** Throws an Error named AbortError (worker.ts:8) once `signal.aborted` is set; any object
+ * with that flag serves (an AbortSignal where the runtime has one). */
+function checkAbort(signal) {
+  if (signal && signal.aborted) {
+    const e = new Error('Stopped by user');
+    e.name = 'AbortError';
+    throw e;
+  }
+}
+
 export class PagedEngine {
   constructor(progress) {
     this.progress = progress || (() => {});
     this.ctx = null; this.model = null; this.source = null; this.gguf = null; this.config = null;
-    this.context = 512; this.batch = 128; this.kvCapacities = [];
+    this.context = 512; this.batch = 16; this.kvCapacities = [];
+    this.budget = null; this.performance = 'low-memory';
     this.busy = false; this.disposed = false; this.tokensInCache = [];
   }
 
   /** PagedEngine.load (engine.ts:51-114): parse, configure, upload, seal. */
-  load(path, options = {}) {
-    const o = Object.assign({ contextLength: 512, batchSize: 128, gpuBudgetMiB: null, device: 0 }, options);
-    this.context = o.contextLength; this.batch = o.batchSize;
+  load(path, options = {}, signal) {
+    const o = Object.assign({ contextLength: 512, gpuBudgetMiB: null, performance: 'low-memory', device: 0 }, options);
+    if (!(o.performance in PRESETS)) throw new Error('Performance must be lite, low-memory or fast.');
+    this.performance = o.performance; this.budget = o.gpuBudgetMiB;
+    this.context = o.contextLength; this.batch = o.batchSize === undefined || o.batchSize === null ? PRESETS[o.performance] : o.batchSize;
     validateContext(this.context);
     if (!BATCHES.includes(this.batch)) throw new Error('Batch size must be 1, 8, 16, 32, 64 or 128.');
     if (o.gpuBudgetMiB !== null && (!Number.isInteger(o.gpuBudgetMiB) || o.gpuBudgetMiB < 512))
@@ -58,6 +74,7 @@ export class PagedEngine {
       const tensors = [...this.gguf.tensors.values()].filter((t) => (t.dims.length === 1 || t.dims.length === 2) &&
         (!t.name.startsWith('blk.') || Number(t.name.split('.')[1]) < c.layers));
       tensors.forEach((t, i) => {
+        checkAbort(signal);
         addon.modelTensor(this.model, t.name, t.type, t.dims, this.source.read(t.offset, t.bytes));
         if (i % 64 === 0) this.progress({ phase: 'loading', detail: 'Uploading weights', fraction: 0.1 + (0.85 * i) / tensors.length });
       });
@@ -72,7 +89,8 @@ export class PagedEngine {
 
   info() {
     return { config: this.config, fileBytes: this.source ? this.source.size : 0, adapter: this.ctx ? addon.adapterName(this.ctx) : '',
-      contextLength: this.context, batchSize: this.batch, stats: this.stats() };
+      contextLength: this.context, gpuBudgetMiB: this.budget, batchSize: this.batch, performance: this.performance,
+      stats: this.stats() };
   }
 
   stats() {
@@ -101,16 +119,22 @@ export class PagedEngine {
   }
 
   /** PagedEngine.generate (engine.ts:257-301), greedy: prefix reuse, output limit, chunked
-   * prefill and the busy guard; the decode loop runs on the device `chunk` tokens at a time. */
-  async *generate(prompt, options = {}, tokenizer = null, chunk = 32) {
+   * prefill and the busy guard; the decode loop runs on the device `chunk` tokens at a time.
+   * A chunk may run past an end-of-turn token; a sliding ring keeps the window plus one
+   * prompt batch, so on models with one the chunk is capped to the batch. An aborted
+   * `signal` stops at the next prompt batch or token and drops the cached prefix. */
+  async *generate(prompt, options = {}, tokenizer = null, chunk = 32, signal = undefined) {
     if (this.busy) throw new Error('A generation is already running.');
     if (this.disposed || !this.model) throw new Error('Load a model first.');
-    const o = Object.assign({ maxTokens: 128, temperature: 0 }, options);
+    const o = Object.assign({ maxTokens: 128, temperature: 0, topK: 40, topP: 0.9 }, options);
     if (!Number.isInteger(o.maxTokens) || o.maxTokens < 1 || o.maxTokens > MAX_CONTEXT) throw new Error(`maxTokens must be 1–${MAX_CONTEXT}.`);
+    if (!Number.isFinite(o.temperature) || o.temperature < 0 || o.temperature > 2 || !Number.isInteger(o.topK) || o.topK < 1 ||
+        o.topK > 200 || !Number.isFinite(o.topP) || o.topP <= 0 || o.topP > 1) throw new Error('Invalid sampling settings.');
     if (o.temperature !== 0) throw new Error('Only greedy decoding (temperature 0) is implemented by this runtime.');
     const ids = tokenizer ? Array.from(tokenizer.chat(prompt)) : Array.from(prompt, Number);
     if (!ids.length) throw new Error('Provide a non-empty prompt.');
     const eos = new Set((tokenizer && tokenizer.eos) || []);
+    if (this.kvCapacities.some((cap) => cap < this.context)) chunk = Math.min(chunk, this.batch);
     this.busy = true;
     try {
       const limit = outputLimit(o.maxTokens, ids.length, this.context);
@@ -122,6 +146,7 @@ export class PagedEngine {
       this.tokensInCache = this.tokensInCache.slice(0, shared);
       let token = -1;
       for (let i = shared; i < ids.length; i += this.batch) {
+        checkAbort(signal);
         const part = ids.slice(i, i + this.batch);
         if (i + part.length === ids.length) token = this.forwardArgmax(part, i);
         else this.forward(part, i, false);
@@ -131,6 +156,7 @@ export class PagedEngine {
       let text = '';
       let pending = [];
       for (let i = 0; i < limit; i++) {
+        checkAbort(signal);
         if (i > 0) {
           if (!pending.length) pending = this.decode(token, this.tokensInCache.length, Math.min(chunk, limit - i));
           this.tokensInCache.push(token);
