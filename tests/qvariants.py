@@ -8,6 +8,8 @@ the three shaped decoders do not use.
 * ``qwen3-mixed``: Q/K norm, partial rotary with linear RoPE scaling, and a Q8_0 K
   projection beside Q4_K Q and Q6_K V (three weight types: the Q/K/V group falls back to
   one launch per matrix).
+* ``llama-q5q4``: the Q5_K_M / Q4_0 mixes of real files: Q5_K Q, K, gate, up and head,
+  Q6_K V (one Q/K/V launch of two types), Q4_0 O, down and embedding table.
 
 Dimensions are the smallest the planar K-quant kernels take: hidden 256 (Q4_K/Q6_K rows of
 whole 256-element blocks), 4 query heads x 64, 2 KV heads, FFN 512, vocab 300. Matrix blocks
@@ -18,10 +20,10 @@ from typing import List, Tuple
 import numpy as np
 
 from webgpu_amd import synth
-from webgpu_amd.gguf import F32, Q4_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
+from webgpu_amd.gguf import F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
 from webgpu_amd.tokenizer import byte_alphabet
 
-KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed")
+KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4")
 
 
 CHAT_SPECIALS = ["<|im_start|>", "<|im_end|>", "<|endoftext|>"]
@@ -46,30 +48,33 @@ def build(kind: str, tokenizer: bool = False):
     file also carries a byte-level BPE vocabulary with a ChatML template."""
     rng = np.random.default_rng(sum(kind.encode()) * 31 + 5)
     H, nh, nkv, hd, F, V, L = 256, 4, 2, 64, 512, 300, 2
-    arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3"}[kind]
+    arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3", "llama-q5q4": "llama"}[kind]
     qd, kd = nh * hd, nkv * hd
     T: List[Tuple[str, List[int], int, np.ndarray]] = []
 
     def mat(name, cols, rows, typ, std=0.05):
         nb = rows * cols // QUANTS[typ]["block"]
-        gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[typ]
+        gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks,
+               Q5_K: synth.q5k_blocks, Q4_0: synth.q4_0_blocks}[typ]
         T.append((name, [cols, rows], typ, gen(rng, nb, std)))
 
     def vec(name, n, center=1.0, spread=0.1):
         v = (center + rng.uniform(-spread, spread, n)).astype(np.float32)
         T.append((name, [n], F32, v.view(np.uint8)))
 
-    mat("token_embd.weight", H, V, Q6_K, 0.5)
+    q5 = kind == "llama-q5q4"
+    mat("token_embd.weight", H, V, Q4_0 if q5 else Q6_K, 0.5)
     vec("output_norm.weight", H)
-    mat("output.weight", H, V, Q6_K, 0.3)
-    k_type = Q8_0 if kind == "qwen3-mixed" else Q4_K
+    mat("output.weight", H, V, Q5_K if q5 else Q6_K, 0.3)
+    k_type = Q8_0 if kind == "qwen3-mixed" else Q5_K if q5 else Q4_K
+    big, small = (Q5_K, Q4_0) if q5 else (Q4_K, Q4_K)
     for l in range(L):
         p = f"blk.{l}."
         vec(p + "attn_norm.weight", H)
-        mat(p + "attn_q.weight", H, qd, Q4_K)
+        mat(p + "attn_q.weight", H, qd, big)
         mat(p + "attn_k.weight", H, kd, k_type)
         mat(p + "attn_v.weight", H, kd, Q6_K)
-        mat(p + "attn_output.weight", qd, H, Q4_K)
+        mat(p + "attn_output.weight", qd, H, small)
         if kind in ("qwen2-bias", "llama-partial"):
             vec(p + "attn_q.bias", qd, 0.0, 0.2)
             vec(p + "attn_k.bias", kd, 0.0, 0.2)
@@ -81,9 +86,9 @@ def build(kind: str, tokenizer: bool = False):
             vec(p + "attn_k_norm.weight", hd)
         vec(p + "ffn_norm.weight", H)
         if kind != "llama-partial":
-            mat(p + "ffn_gate.weight", H, F, Q4_K)
-        mat(p + "ffn_up.weight", H, F, Q4_K)
-        mat(p + "ffn_down.weight", F, H, Q4_K)
+            mat(p + "ffn_gate.weight", H, F, big)
+        mat(p + "ffn_up.weight", H, F, big)
+        mat(p + "ffn_down.weight", F, H, small)
     meta = [("general.architecture", 8, arch), ("general.name", 8, kind),
             (f"{arch}.block_count", 4, L), (f"{arch}.context_length", 4, 4096),
             (f"{arch}.embedding_length", 4, H), (f"{arch}.feed_forward_length", 4, F),
@@ -95,6 +100,8 @@ def build(kind: str, tokenizer: bool = False):
     elif kind == "llama-partial":
         meta += [(f"{arch}.rope.freq_base", 6, 1e4), (f"{arch}.rope.dimension_count", 4, 32),
                  (f"{arch}.attention.sliding_window", 4, 24)]
+    elif kind == "llama-q5q4":
+        meta += [(f"{arch}.rope.freq_base", 6, 5e5), (f"{arch}.rope.dimension_count", 4, hd)]
     else:
         meta += [(f"{arch}.rope.freq_base", 6, 1e6), (f"{arch}.rope.dimension_count", 4, 48),
                  (f"{arch}.rope.scaling.type", 8, "linear"), (f"{arch}.rope.scaling.factor", 6, 2.0)]

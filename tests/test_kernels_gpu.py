@@ -19,6 +19,9 @@ from webgpu_amd.gpu import WgdError, WGD_E_NONFINITE
 
 pytestmark = pytest.mark.gpu
 ALL = [F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K]
+# synthetic block generators of the types with a planar layout
+GEN = {Q4_K: synth.q4k_blocks, Q5_K: synth.q5k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks,
+       Q4_0: synth.q4_0_blocks}
 
 
 def near(got, want, tol=1e-3, label=""):
@@ -90,10 +93,11 @@ def test_matmul_offsets_all_types(gpu, type_, batch):
 
 @pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 1024, 14336), (Q4_K, 3072, 1024),
                                              (Q6_K, 1024, 4096), (Q6_K, 520, 5376), (Q8_0, 512, 4096),
-                                             (Q4_K, 300, 3072)])
+                                             (Q4_K, 300, 3072), (Q5_K, 1024, 4096), (Q5_K, 520, 14336),
+                                             (Q4_0, 512, 4096), (Q4_0, 300, 3136)])
 def test_fast_matvec_real_shapes(gpu, type_, rows, cols):
     rng = np.random.default_rng(rows + cols)
-    gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+    gen = GEN[type_]
     w = gen(rng, rows * cols // QUANTS[type_]["block"])
     x = rng.standard_normal(cols).astype(np.float32)
     want = orc.matmul(type_, w, x, cols, rows, rows, 0, 0, 1)
@@ -106,11 +110,11 @@ def test_fast_matvec_real_shapes(gpu, type_, rows, cols):
         gpu.destroy(buf)
 
 
-@pytest.mark.parametrize("type_", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("type_", [Q4_K, Q5_K, Q6_K, Q8_0, Q4_0])
 def test_prompt_gemm_on_mfma(gpu, type_):
     rng = np.random.default_rng(7 + type_)
     rows, cols, batch = 200, 1024, 77
-    gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+    gen = GEN[type_]
     w = gen(rng, rows * cols // QUANTS[type_]["block"])
     x = rng.standard_normal((batch + 2) * cols).astype(np.float32)
     want = orc.matmul(type_, w, x, cols, rows, rows, 0, 2, batch)
@@ -123,13 +127,32 @@ def test_prompt_gemm_on_mfma(gpu, type_):
             gpu.destroy(buf)
 
 
+@pytest.mark.parametrize("type_", [Q8_0, Q4_0])
+def test_widths_outside_the_planar_tiles_stay_in_the_gguf_layout(gpu, type_):
+    # 96 columns is not a whole 64-column GEMM tile: the matrix keeps its GGUF layout and
+    # every batch runs the generic kernels on it
+    rng = np.random.default_rng(96 + type_)
+    rows, cols = 40, 96
+    w = GEN[type_](rng, rows * cols // 32)
+    for batch in (1, 70):
+        x = rng.standard_normal(batch * cols).astype(np.float32)
+        want = orc.matmul(type_, w, x, cols, rows, rows, 0, 0, batch)
+        wb = gpu.upload_weights(type_, cols, rows, w)
+        xb, yb = gpu.upload(x, "x"), gpu.buffer(batch * rows * 4, "y")
+        gpu.matmul(type_, wb, xb, yb, cols, rows, rows, 0, 0, batch)
+        near(gpu.read_f32(yb, batch * rows), want, 1e-4, f"{type_} width 96 batch {batch}")
+        for buf in (wb, xb, yb):
+            gpu.destroy(buf)
+
+
 @pytest.mark.parametrize("type_,rows,cols,batch", [(Q4_K, 4096, 4096, 128), (Q6_K, 1024, 4096, 130),
-                                                   (Q8_0, 384, 2048, 128), (Q4_K, 640, 14336, 64)])
+                                                   (Q8_0, 384, 2048, 128), (Q4_K, 640, 14336, 64),
+                                                   (Q5_K, 1024, 4096, 128), (Q4_0, 512, 4096, 130)])
 def test_prompt_gemm_real_shapes(gpu, type_, rows, cols, batch):
     """Planar prompt GEMM at layer shapes: whole 128-token tiles, a second token tile,
     split-K partial sums, a row offset inside a wider output (stride/rowBase, verify.ts:16-38)."""
     rng = np.random.default_rng(rows * 3 + cols + batch)
-    gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+    gen = GEN[type_]
     w = gen(rng, rows * cols // QUANTS[type_]["block"])
     x = rng.standard_normal((batch + 1) * cols).astype(np.float32)
     stride, base = rows + 8, 5
@@ -288,14 +311,14 @@ def test_argmax_rules(gpu):
 
 
 # ---------------------------------------------------------------- embedding gather
-@pytest.mark.parametrize("type_", [F32, Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("type_", [F32, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0])
 def test_embed_gather_bit_exact(gpu, type_):
     rng = np.random.default_rng(type_)
     hidden, rows = 512, 40
     if type_ == F32:
         table = rng.standard_normal(hidden * rows).astype(np.float32).view(np.uint8).copy()
     else:
-        gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+        gen = GEN[type_]
         table = gen(rng, hidden * rows // QUANTS[type_]["block"])
     ids = np.array([3, 0, 39, 3, 17], np.int32)
     full = orc.dequant(table, type_, hidden * rows, f32=False).reshape(rows, hidden)
@@ -342,11 +365,12 @@ def test_bounds_checks_reject_overruns(gpu):
 
 
 # ---------------------------------------------------------------- quantized activation + matvec entries
-@pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 512, 4096), (Q6_K, 256, 5376), (Q8_0, 128, 1024)])
+@pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 512, 4096), (Q6_K, 256, 5376), (Q8_0, 128, 1024),
+                                             (Q5_K, 256, 4096), (Q4_0, 128, 2048)])
 def test_quantize_with_rms_norm_then_matvec(gpu, type_, rows, cols):
     """wgd_quantize(x, norm w) + wgd_matvec == W @ (x * rsqrt(mean(x^2) + eps) * w)."""
     rng = np.random.default_rng(rows)
-    gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks}[type_]
+    gen = GEN[type_]
     w = gen(rng, rows * cols // QUANTS[type_]["block"])
     x = (rng.standard_normal(cols) * 3).astype(np.float32)
     nw = (1 + rng.uniform(-0.1, 0.1, cols)).astype(np.float32)

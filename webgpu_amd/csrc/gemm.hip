@@ -99,6 +99,39 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
     }
     return;
   }
+  if (a.type == Q5_K && a.layout == LAYOUT_PLANAR) {
+    const Q5Planes p = q5_planes(a.nbt);
+    const uint32_t j = k & 255, s = j >> 5, e0 = k & 31;
+    uint4 h = *(const uint4 *)(a.w + p.hdr + tiled(row, k >> 8, a.bpr) * 16);
+    uint2 qv = *(const uint2 *)(a.w + p.qs + tiled(row, k >> 5, a.bpr * 8) * 16 + (e0 & 15));
+    const uint32_t hb = *(const uint32_t *)(a.w + p.qh + tiled(row, k >> 5, a.bpr * 8) * 4);
+    uint32_t A = h.y, B = h.z, C = h.w, sh = 8 * (s & 3), sc, m;
+    if (s < 4) { sc = (A >> sh) & 63u; m = (B >> sh) & 63u; }
+    else { sc = ((C >> sh) & 15u) | (((A >> sh) >> 6 & 3u) << 4); m = ((C >> sh) >> 4 & 15u) | (((B >> sh) >> 6 & 3u) << 4); }
+    float dsc = half_bits(h.x & 0xFFFFu) * (float)sc, dmm = half_bits(h.x >> 16) * (float)m;
+    uint32_t sq = 4 * (e0 >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      // fifth bit of chunk element e: byte e % 4, bit e / 4 (e < 16) or 4 + (e - 16) / 4
+      const uint32_t e = e0 + i, pos = 8 * (e & 3) + (e < 16 ? e / 4 : 4 + (e - 16) / 4);
+      uint32_t byte = ((i < 4 ? qv.x : qv.y) >> (8 * (i & 3))) & 0xFFu;
+      o[i] = dsc * (float)(((byte >> sq) & 15u) | (((hb >> pos) & 1u) << 4)) - dmm;
+    }
+    return;
+  }
+  if (a.type == Q4_0 && a.layout == LAYOUT_PLANAR) {
+    const Q40Planes p = q40_planes(a.nbt);
+    const uint32_t e0 = k & 31;
+    uint2 qv = *(const uint2 *)(a.w + p.qs + tiled(row, k >> 5, a.bpr) * 16 + (e0 & 15));
+    float d = half_bits(*(const uint16_t *)(a.w + p.d + tiled(row, k >> 5, a.bpr) * 2));
+    uint32_t sq = 4 * (e0 >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t byte = ((i < 4 ? qv.x : qv.y) >> (8 * (i & 3))) & 0xFFu;
+      o[i] = d * (float)((int)((byte >> sq) & 15u) - 8);
+    }
+    return;
+  }
   if (a.type == Q8_0 && a.layout == LAYOUT_PLANAR) {
     const Q8Planes p = q8_planes(a.nbt);
     uint2 q = *(const uint2 *)(a.w + p.qs + tiled(row, k >> 4, a.bpr * 2) * 16 + (k & 15));
@@ -183,7 +216,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 
 // ------------------------------------------------------------------ planar K-quant GEMM
 //
-// The prompt GEMM of the planar layouts (Q4_K, Q6_K, Q8_0; the decode matvec's weights). A
+// The prompt GEMM of the planar layouts (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0; the decode matvec's weights). A
 // workgroup owns QG_M = 128 weight rows x QG_N = 128 tokens and a K span (split-K when the
 // rows alone give too few workgroups; partial sums are added in split order by
 // k_gemm_reduce, so results do not depend on timing). The activations are split into bf16
@@ -314,6 +347,56 @@ template <> struct QWeights<Q8_0> {
 #pragma unroll
         for (int b = 0; b < 4; b++) v[16 * u + 4 * k + b] = dd * (float)(int8_t)((qw[k] >> (8 * b)) & 0xFFu);
     }
+  }
+};
+
+// Q5_K: Q4_K's chunk and header planes (the header after the fifth-bit plane) and the
+// chunk's dword of fifth bits, moved to bit 4 of each quant byte (quant.ts:13-19).
+template <> struct QWeights<Q5_K> {
+  uint4 q, h; uint32_t b;
+  __device__ void fetch(const QJob &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+    const uint32_t tc = (T * a.C + c) * 16 + r;
+    q = qld16(rw, tc * 16);
+    b = __builtin_amdgcn_raw_buffer_load_b32(rw, a.nbp * 128 + tc * 4, 0, 0);
+    h = qld16(rw, a.nbp * 160 + ((T * a.bpr + c / 8) * 16 + r) * 16);
+  }
+  __device__ void values(uint32_t c, float *v) const {
+    const uint32_t s = c & 7, sh = 8 * (s & 3);
+    uint32_t sc, m;
+    if (s < 4) { sc = (h.y >> sh) & 63u; m = (h.z >> sh) & 63u; }
+    else { sc = ((h.w >> sh) & 15u) | (((h.y >> sh) >> 6 & 3u) << 4); m = ((h.w >> sh) >> 4 & 15u) | (((h.z >> sh) >> 6 & 3u) << 4); }
+    const float dsc = half_bits(h.x & 0xFFFFu) * (float)sc, dmm = half_bits(h.x >> 16) * (float)m;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t lo = (qw[k] & 0x0F0F0F0Fu) | ((b << (4 - k)) & 0x10101010u);
+      const uint32_t hi = ((qw[k] >> 4) & 0x0F0F0F0Fu) | ((b >> k) & 0x10101010u);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[4 * k + e] = fmaf(dsc, (float)((lo >> (8 * e)) & 0xFFu), -dmm);
+        v[16 + 4 * k + e] = fmaf(dsc, (float)((hi >> (8 * e)) & 0xFFu), -dmm);
+      }
+    }
+  }
+};
+// Q4_0: one block per chunk, d * (q - 8) (quant.ts:7).
+template <> struct QWeights<Q4_0> {
+  uint4 q; uint32_t d;
+  __device__ void fetch(const QJob &a, QRsrc rw, uint32_t T, uint32_t r, uint32_t c) {
+    const uint32_t tc = (T * a.C + c) * 16 + r;
+    q = qld16(rw, tc * 16);
+    d = __builtin_amdgcn_raw_buffer_load_b16(rw, a.nbp * 16 + tc * 2, 0, 0);
+  }
+  __device__ void values(uint32_t, float *v) const {
+    const float dd = half_bits(d & 0xFFFFu);
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[4 * k + e] = dd * (float)((int)((qw[k] >> (8 * e)) & 15u) - 8);
+        v[16 + 4 * k + e] = dd * (float)((int)((qw[k] >> (8 * e + 4)) & 15u) - 8);
+      }
   }
 };
 
@@ -461,8 +544,16 @@ __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t 
 
 static bool qgemm_supported(const Matrix &w) {
   if (w.layout != LAYOUT_PLANAR) return false;
-  if (w.type == Q4_K || w.type == Q6_K) return w.cols % 256 == 0;
-  return w.type == Q8_0 && w.cols % QG_K == 0;
+  if (w.type == Q4_K || w.type == Q5_K || w.type == Q6_K) return w.cols % 256 == 0;
+  return (w.type == Q8_0 || w.type == Q4_0) && w.cols % QG_K == 0;
+}
+
+// The type pairs (t0 <= t1) with a grouped kernel: every type alone, and the mixes of real
+// checkpoints (K-quant projections beside Q6_K or Q8_0 ones).
+static bool qgemm_pair(int a, int b) {
+  if (a == b) return true;
+  return (a == Q4_K && b == Q6_K) || (a == Q8_0 && b == Q4_K) || (a == Q8_0 && b == Q6_K) ||
+         (a == Q4_K && b == Q5_K) || (a == Q5_K && b == Q6_K);
 }
 
 // The launch's two weight types (t[0] <= t[1]); false for more than two.
@@ -487,7 +578,7 @@ bool gemm_group_ok(const GemmGroup &g, uint32_t batch) {
       return false;
   if (g.glu_out && (g.n != 2 || g.job[0].w->rows != g.job[1].w->rows || g.job[0].w->rows % QG_K)) return false;
   int t[2];
-  return group_types(g, t);
+  return group_types(g, t) && qgemm_pair(t[0], t[1]);
 }
 
 // K span per workgroup: enough splits for two workgroups per CU (64 KB of LDS each), each
@@ -497,7 +588,7 @@ static uint32_t group_kspan(const GemmGroup &g, uint32_t batch, uint64_t scratch
   uint32_t align = QG_K, tiles = 0, rows = 0;
   for (uint32_t j = 0; j < g.n; j++) {
     const Matrix &w = *g.job[j].w;
-    if (w.type != Q8_0) align = 256;
+    if (w.type != Q8_0 && w.type != Q4_0) align = 256;
     tiles += (w.rows + QG_M - 1) / QG_M;
     rows += w.rows;
   }
@@ -590,6 +681,10 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
   else if (a == Q4_K && b == Q6_K) launch_qgemm<Q4_K, Q6_K>(s, grid, q);
   else if (a == Q8_0 && b == Q4_K) launch_qgemm<Q8_0, Q4_K>(s, grid, q);
   else if (a == Q8_0 && b == Q6_K) launch_qgemm<Q8_0, Q6_K>(s, grid, q);
+  else if (a == Q5_K && b == Q5_K) launch_qgemm<Q5_K, Q5_K>(s, grid, q);
+  else if (a == Q4_0 && b == Q4_0) launch_qgemm<Q4_0, Q4_0>(s, grid, q);
+  else if (a == Q4_K && b == Q5_K) launch_qgemm<Q4_K, Q5_K>(s, grid, q);
+  else if (a == Q5_K && b == Q6_K) launch_qgemm<Q5_K, Q6_K>(s, grid, q);
   else return hipErrorInvalidValue;
   WGD_HIP(hipGetLastError());
   if (g.glu_out) {

@@ -54,9 +54,17 @@ struct Q6Planes { uint64_t ql, qh, sc, d; };
 __host__ __device__ inline Q6Planes q6_planes(uint64_t nbp) { return {0, nbp * 128, nbp * 192, nbp * 208}; }
 struct Q8Planes { uint64_t qs, d; };
 __host__ __device__ inline Q8Planes q8_planes(uint64_t nbp) { return {0, nbp * 32}; }
+// Q5_K: the Q4_K nibble chunks, one dword of fifth bits per chunk, the 16-byte header.
+struct Q5Planes { uint64_t qs, qh, hdr; };
+__host__ __device__ inline Q5Planes q5_planes(uint64_t nbp) { return {0, nbp * 128, nbp * 160}; }
+// Q4_0: a block is one chunk; its 16 quant bytes, then d per block.
+struct Q40Planes { uint64_t qs, d; };
+__host__ __device__ inline Q40Planes q40_planes(uint64_t nbp) { return {0, nbp * 16}; }
 __host__ __device__ inline uint32_t chunk_elems(int type) { return type == Q8_0 ? 16u : 32u; }
 
-bool has_planar(int type);
+// Whether matrices of this type and width are stored in the planar layout: the K-quants,
+// and Q8_0 / Q4_0 in whole 64-column tiles (the prompt GEMM's K tile).
+bool has_planar(int type, uint64_t cols);
 // Bytes of a planar matrix (rows padded to 16).
 uint64_t planar_bytes(int type, uint32_t cols, uint32_t rows);
 // Rewrites a GGUF matrix (rows x cols) into the planar layout (device to device); dst must

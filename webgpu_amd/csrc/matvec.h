@@ -132,6 +132,8 @@ struct MV {
 };
 
 bool mv_supported(const Matrix &w);
+// Whether segments of these two weight types can share one matvec launch.
+bool mv_mixable(int a, int b);
 // Number of argmax keys a single-matrix MV_STORE launch of w writes to MVOut::arg_part.
 uint32_t mv_arg_entries(const Matrix &w);
 MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out);

@@ -5,7 +5,7 @@
 // is quantized first ("QX" format): per 16-element block a scale s = max|x| / 127 and three
 // signed base-254 digits per element, x = s * (d0 + d1/254 + d2/254^2) (error <= 6.1e-8 *
 // max|x|, f32-level). Weights stay in their raw form: 4-bit (Q4_K), 6-bit (Q6_K) or 8-bit
-// (Q8_0) quants become int8 operands of v_mfma_i32_16x16x64_i8, whose int32 sums are exact.
+// (Q8_0) quants, and 5-bit (Q5_K) and 4-bit offset (Q4_0) ones, become int8 operands of v_mfma_i32_16x16x64_i8, whose int32 sums are exact.
 // Block scales apply once per 16 elements; the Q4_K minimum and the Q6_K offset use the
 // exact sums of x.
 //
@@ -30,6 +30,7 @@
 // write back and invalidate it.
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 #include "internal.h"
 #include "decode.h"
@@ -72,6 +73,9 @@ __device__ __forceinline__ uint4 bl16(Rsrc r, uint32_t v, uint32_t s) {
 __device__ __forceinline__ uint2 bl8(Rsrc r, uint32_t v, uint32_t s) {
   const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(r, v, s, CPOL_NT);
   return make_uint2(x.x, x.y);
+}
+__device__ __forceinline__ uint32_t bl4(Rsrc r, uint32_t v, uint32_t s) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, CPOL_NT);
 }
 __device__ __forceinline__ uint32_t bl2(Rsrc r, uint32_t v, uint32_t s) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, v, s, CPOL_NT);
@@ -199,6 +203,73 @@ struct CQ80 {
   static __device__ __forceinline__ float dot(const W &r, const L &, const XA &x) {
     const v4i b0 = {(int)r.q0.x, (int)r.q0.y, (int)r.q0.z, (int)r.q0.w}, b1 = {(int)r.q1.x, (int)r.q1.y, (int)r.q1.z, (int)r.q1.w};
     return fmaf(f16lo(r.d1) * x.s[1][0], dig8(mfma_i8(x.a[1][0], b1)), f16lo(r.d0) * x.s[0][0] * dig8(mfma_i8(x.a[0][0], b0)));
+  }
+};
+
+// Q5_K: Q4_K with a fifth bit per quant (quant.ts:13-19). The low nibbles and the header
+// are laid out as for Q4_K; each chunk's fifth bits are one dword whose byte b holds, at bit
+// k, element 4k + b and at bit 4 + k element 16 + 4k + b, so one shift and mask per operand
+// dword moves four of them to bit 4 of their bytes. Quants reach 31: the digit sums take
+// the f32 last step.
+struct CQ5K {
+  static constexpr int N = 32;
+  struct W { uint4 q0, q1, h; uint32_t b0, b1; };
+  struct L { uint32_t vq, vb, vh, g8; };
+  static __device__ __forceinline__ L lane(uint32_t r, uint32_t g) { return L{256 * g + 16 * r, 64 * g + 4 * r, 16 * r, 8 * g}; }
+  static __device__ __forceinline__ W load(Rsrc w, const MVSeg &s, uint32_t C, const Unit &u, const L &l) {
+    W r;
+    const uint32_t tc = u.T * C + u.cb;
+    r.q0 = bl16(w, l.vq, 256 * tc);
+    r.q1 = bl16(w, l.vq + 1024, 256 * tc);
+    r.b0 = bl4(w, l.vb, s.nbp * 128 + 64 * tc);
+    r.b1 = bl4(w, l.vb + 256, s.nbp * 128 + 64 * tc);
+    r.h = bl16(w, l.vh, s.nbp * 160 + 256 * (u.T * s.bpr + u.cb / 8));
+    return r;
+  }
+  static __device__ __forceinline__ float chunk(const uint4 &qq, uint32_t B, const v4i (&a)[2], const float (&sx)[2]) {
+    const uint32_t q[4] = {qq.x, qq.y, qq.z, qq.w};
+    v4i lo, hi;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      lo[k] = (int)((q[k] & M4) | ((B << (4 - k)) & 0x10101010u));
+      hi[k] = (int)(((q[k] >> 4) & M4) | ((B >> k) & 0x10101010u));
+    }
+    return fmaf(sx[1], dig8(mfma_i8(a[1], hi)), sx[0] * dig8(mfma_i8(a[0], lo)));
+  }
+  static __device__ __forceinline__ float dot(const W &r, const L &l, const XA &x) {
+    const float ca = chunk(r.q0, r.b0, x.a[0], x.s[0]), cb = chunk(r.q1, r.b1, x.a[1], x.s[1]);
+    const uint32_t sca = __builtin_amdgcn_ubfe(r.h.y, l.g8, 6), mna = __builtin_amdgcn_ubfe(r.h.z, l.g8, 6);
+    const uint32_t scb = __builtin_amdgcn_ubfe(r.h.w, l.g8, 4) | (__builtin_amdgcn_ubfe(r.h.y, l.g8 + 6, 2) << 4);
+    const uint32_t mnb = __builtin_amdgcn_ubfe(r.h.w, l.g8 + 4, 4) | (__builtin_amdgcn_ubfe(r.h.z, l.g8 + 6, 2) << 4);
+    const float u = fmaf((float)scb, cb, (float)sca * ca);
+    const float v = fmaf((float)mnb, x.m[1][0] + x.m[1][1], (float)mna * (x.m[0][0] + x.m[0][1]));
+    return fmaf(f16lo(r.h.x), u, -f16hi(r.h.x) * v);
+  }
+};
+
+// Q4_0: a chunk is a whole block, d * (q - 8) (quant.ts:7); the offset uses the exact
+// block sums of x. A lane's chunk columns cb + g and cb + 4 + g are blocks of their own.
+struct CQ40 {
+  static constexpr int N = 32;
+  struct W { uint4 q0, q1; uint32_t d0, d1; };
+  struct L { uint32_t vq, vd; };
+  static __device__ __forceinline__ L lane(uint32_t r, uint32_t g) { return L{256 * g + 16 * r, 32 * g + 2 * r}; }
+  static __device__ __forceinline__ W load(Rsrc w, const MVSeg &s, uint32_t C, const Unit &u, const L &l) {
+    W r;
+    const uint32_t tc = u.T * C + u.cb;
+    r.q0 = bl16(w, l.vq, 256 * tc);
+    r.q1 = bl16(w, l.vq + 1024, 256 * tc);
+    r.d0 = bl2(w, l.vd, s.nbp * 16 + 32 * tc);
+    r.d1 = bl2(w, l.vd + 128, s.nbp * 16 + 32 * tc);
+    return r;
+  }
+  static __device__ __forceinline__ float chunk(const uint4 &q, const v4i (&a)[2], const float (&sx)[2], const float (&mx)[2]) {
+    const v4i lo = {(int)(q.x & M4), (int)(q.y & M4), (int)(q.z & M4), (int)(q.w & M4)};
+    const v4i hi = {(int)((q.x >> 4) & M4), (int)((q.y >> 4) & M4), (int)((q.z >> 4) & M4), (int)((q.w >> 4) & M4)};
+    return fmaf(sx[1], dig4(mfma_i8(a[1], hi)), fmaf(sx[0], dig4(mfma_i8(a[0], lo)), -8.f * (mx[0] + mx[1])));
+  }
+  static __device__ __forceinline__ float dot(const W &r, const L &, const XA &x) {
+    return fmaf(f16lo(r.d1), chunk(r.q1, x.a[1], x.s[1], x.m[1]), f16lo(r.d0) * chunk(r.q0, x.a[0], x.s[0], x.m[0]));
   }
 };
 
@@ -493,9 +564,15 @@ hipError_t quantize(hipStream_t s, const float *x, uint32_t K, const float *norm
 
 bool mv_supported(const Matrix &w) {
   if (w.layout != LAYOUT_PLANAR || !w.cols || !w.rows) return false;
-  if (w.type == Q4_K || w.type == Q6_K) return w.cols % 256 == 0;
-  if (w.type == Q8_0) return w.cols % 32 == 0;
+  if (w.type == Q4_K || w.type == Q5_K || w.type == Q6_K) return w.cols % 256 == 0;
+  if (w.type == Q8_0 || w.type == Q4_0) return w.cols % 32 == 0;
   return false;
+}
+
+bool mv_mixable(int a, int b) {
+  if (a == b) return true;
+  if (a > b) std::swap(a, b);
+  return (a == Q4_K || a == Q5_K) && b == Q6_K;
 }
 
 static uint32_t lds_limit() { return 160 * 1024; }
@@ -521,7 +598,7 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
   static const int env_du = getenv("WGD_MV_DU") ? atoi(getenv("WGD_MV_DU")) : 0;
   const uint32_t dumax = glu ? 2 : 4;
   // unique weight bytes of one unit (16 rows x 8 chunk columns and its scale planes), KB
-  const double unit_kb = w.type == Q6_K ? 2.625 : w.type == Q4_K ? 2.25 : 2.125;
+  const double unit_kb = w.type == Q6_K ? 2.625 : w.type == Q5_K ? 2.75 : w.type == Q8_0 ? 2.125 : 2.25;
   double best_cost = 1e30;
   for (uint32_t ns = 1; ns <= 16; ns++) {
     if (env_ns && (int)ns != env_ns) continue;
@@ -599,13 +676,13 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   if ((epi == MV_SILU || epi == MV_GELU) != glu) return hipErrorInvalidValue;
   if (x.len != w0.cols) return hipErrorInvalidValue;
   uint32_t rows[MV_MAX_SEGS];
-  // Q4_K and Q6_K segments may share a launch (same chunk shape); other types run alone
-  const bool kq0 = w0.type == Q4_K || w0.type == Q6_K;
+  // Q6_K segments may share a launch with Q4_K or Q5_K ones (same chunk shape); other
+  // types run alone
   int other = -1;
   for (uint32_t i = 0; i < n; i++) {
     const Matrix &w = *t[i].w;
     if (w.type != w0.type) {
-      if (!kq0 || !(w.type == Q4_K || w.type == Q6_K) || glu) return hipErrorInvalidValue;
+      if ((other >= 0 && w.type != other) || !mv_mixable(w0.type, w.type) || glu) return hipErrorInvalidValue;
       other = w.type;
     }
     if (!mv_supported(w) || w.cols != w0.cols || !t[i].y) return hipErrorInvalidValue;
@@ -649,12 +726,18 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
     if (n != 1) return hipErrorInvalidValue;
     m.arg_part = out->arg_part;
   }
-  if (other == Q6_K) return launch_t<CQ4K, CQ6K, false>(s, m, p);  // w0 is Q4_K
-  if (other == Q4_K) return launch_t<CQ6K, CQ4K, false>(s, m, p);
+  if (other >= 0) {
+    if (w0.type == Q4_K) return launch_t<CQ4K, CQ6K, false>(s, m, p);
+    if (w0.type == Q5_K) return launch_t<CQ5K, CQ6K, false>(s, m, p);
+    if (other == Q4_K) return launch_t<CQ6K, CQ4K, false>(s, m, p);
+    return launch_t<CQ6K, CQ5K, false>(s, m, p);
+  }
   switch (w0.type) {
     case Q4_K: return glu ? launch_t<CQ4K, CQ4K, true>(s, m, p) : launch_t<CQ4K, CQ4K, false>(s, m, p);
+    case Q5_K: return glu ? launch_t<CQ5K, CQ5K, true>(s, m, p) : launch_t<CQ5K, CQ5K, false>(s, m, p);
     case Q6_K: return glu ? launch_t<CQ6K, CQ6K, true>(s, m, p) : launch_t<CQ6K, CQ6K, false>(s, m, p);
     case Q8_0: return glu ? launch_t<CQ80, CQ80, true>(s, m, p) : launch_t<CQ80, CQ80, false>(s, m, p);
+    case Q4_0: return glu ? launch_t<CQ40, CQ40, true>(s, m, p) : launch_t<CQ40, CQ40, false>(s, m, p);
   }
   return hipErrorInvalidValue;
 }

@@ -375,18 +375,22 @@ __global__ __launch_bounds__(256) void k_argmax_advance(const uint64_t *part, ui
 
 QXView qv(void *p, uint32_t K, bool normed = false, float eps = 0.f) { return qx_const(qx_view(p, K), K, normed, eps); }
 
-// Matvecs of several matrices that read the same activation: one launch for K-quants
-// (Q4_K and Q6_K mix), else one per weight type.
+// Matvecs of several matrices that read the same activation: one launch per group of at
+// most two types that mix (Q6_K with Q4_K or Q5_K), else one per weight type.
 hipError_t mv_group(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x) {
-  auto kq = [](int type) { return type == Q4_K || type == Q6_K; };
-  auto same = [&](int a, int b) { return a == b || (kq(a) && kq(b)); };
   bool done[MV_MAX_SEGS] = {};
   for (uint32_t i = 0; i < n; i++) {
     if (done[i]) continue;
     MVTarget grp[MV_MAX_SEGS];
     uint32_t k = 0;
-    for (uint32_t j = i; j < n; j++)
-      if (!done[j] && same(t[j].w->type, t[i].w->type)) { grp[k++] = t[j]; done[j] = true; }
+    const int a = t[i].w->type;
+    int b = a;
+    for (uint32_t j = i; j < n; j++) {
+      const int ty = t[j].w->type;
+      if (done[j]) continue;
+      if (ty != a && b == a && mv_mixable(a, ty)) b = ty;
+      if (ty == a || ty == b) { grp[k++] = t[j]; done[j] = true; }
+    }
     WGD_HIP(mv(s, grp, k, x, MV_STORE));
   }
   return hipSuccess;
@@ -640,9 +644,9 @@ int wgd_model_tensor(wgd_model *m, const char *name, int32_t type, int32_t n_dim
   if (ne0 > 0xFFFFFFFFull || ne1 > 0xFFFFFFFFull) return fail(ctx, WGD_E_INVALID, "%s: too large", name);
   Matrix mat; mat.type = type; mat.cols = (uint32_t)ne0; mat.rows = (uint32_t)ne1;
   void *dev = nullptr;
-  int rc = alloc(m, has_planar(type) ? planar_bytes(type, mat.cols, mat.rows) : need, label, &dev);
+  int rc = alloc(m, has_planar(type, mat.cols) ? planar_bytes(type, mat.cols, mat.rows) : need, label, &dev);
   if (rc) return rc;
-  if (has_planar(type)) {
+  if (has_planar(type, mat.cols)) {
     void *raw = nullptr;
     rc = ctx_alloc(ctx, need, "upload staging", &raw);
     if (rc) return rc;

@@ -60,6 +60,22 @@ __device__ __forceinline__ float deq_planar(int type, const uint8_t *w, uint64_t
     const uint32_t q = q4_quant(w, row, cols / 32, i);
     return half_bits(h[0] | ((uint32_t)h[1] << 8)) * (float)(sc * q) - half_bits(h[2] | ((uint32_t)h[3] << 8)) * (float)mn;
   }
+  if (type == Q5_K) {
+    const Q5Planes p = q5_planes(nbp);
+    const uint8_t *h = w + p.hdr + tiled(row, i / 256, bpr) * 16;
+    const uint32_t j = i % 256, s = j / 32, e = i % 32;
+    uint32_t sc, mn;
+    if (s < 4) { sc = h[4 + s] & 63u; mn = h[8 + s] & 63u; }
+    else { sc = (h[8 + s] & 15u) | ((h[s] >> 6) << 4); mn = (h[8 + s] >> 4) | ((h[4 + s] >> 6) << 4); }
+    const uint8_t *qh = w + p.qh + tiled(row, i / 32, cols / 32) * 4;
+    const uint32_t bit = e < 16 ? 8 * (e % 4) + e / 4 : 8 * ((e - 16) % 4) + 4 + (e - 16) / 4;
+    const uint32_t q = q4_quant(w, row, cols / 32, i) | (((qh[bit / 8] >> (bit % 8)) & 1u) << 4);
+    return half_bits(h[0] | ((uint32_t)h[1] << 8)) * (float)(sc * q) - half_bits(h[2] | ((uint32_t)h[3] << 8)) * (float)mn;
+  }
+  if (type == Q4_0) {
+    const uint64_t d = q40_planes(nbp).d + tiled(row, i / 32, bpr) * 2;
+    return half_bits(w[d] | ((uint32_t)w[d + 1] << 8)) * (float)((int)q4_quant(w, row, cols / 32, i) - 8);
+  }
   if (type == Q6_K) {
     const Q6Planes p = q6_planes(nbp);
     const uint32_t C = cols / 32;
@@ -134,7 +150,10 @@ hipError_t token_start(hipStream_t s, const Matrix &embd, const int32_t *token, 
 
 // ------------------------------------------------------------------ planar repack
 
-bool has_planar(int type) { return type == Q4_K || type == Q6_K || type == Q8_0; }
+bool has_planar(int type, uint64_t cols) {
+  if (type == Q4_K || type == Q5_K || type == Q6_K) return cols % 256 == 0;
+  return (type == Q8_0 || type == Q4_0) && cols % 64 == 0;
+}
 
 uint64_t planar_bytes(int type, uint32_t cols, uint32_t rows) { return tile_rows(rows) * row_bytes(type, cols); }
 
@@ -210,14 +229,58 @@ __global__ void k_repack_q8(const uint8_t *src, uint8_t *dst, uint32_t bpr, uint
   }
 }
 
+// Q5_K: the low nibbles as Q4_K's chunks (GGUF quant bytes at 48); the fifth bits (bit e / 32
+// of GGUF byte 16 + e % 32) as one dword per chunk, element e < 16 at bit 8 (e % 4) + e / 4 and
+// element 16 + e at bit 8 (e % 4) + 4 + e / 4, so the bits of four consecutive elements sit
+// at the same position of four bytes; the 16-byte header (d, dmin, scales) copied.
+__device__ __forceinline__ uint32_t q5_bit_pos(uint32_t e) {
+  return e < 16 ? 8 * (e % 4) + e / 4 : 8 * ((e - 16) % 4) + 4 + (e - 16) / 4;
+}
+__global__ void k_repack_q5(const uint8_t *src, uint8_t *dst, uint32_t bpr, uint32_t rows) {
+  const uint64_t nb = (uint64_t)rows * bpr, nbp = tile_rows(rows) * bpr;
+  const uint32_t C = bpr * 8;
+  const Q5Planes p = q5_planes(nbp);
+  for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t row = (uint32_t)(blk / bpr), b = (uint32_t)(blk % bpr);
+    const uint8_t *s = src + blk * 176;
+    uint8_t *h = dst + p.hdr + tiled(row, b, bpr) * 16;
+    for (int o = 0; o < 16; o++) h[o] = s[o];
+    auto q = [&](uint32_t e) -> uint32_t { return (s[48 + 32 * (e / 64) + e % 32] >> (4 * ((e % 64) / 32))) & 15u; };
+    for (uint32_t j = 0; j < 8; j++) {
+      const uint64_t ci = tiled(row, 8 * b + j, C);
+      for (uint32_t i = 0; i < 16; i++) dst[p.qs + ci * 16 + i] = (uint8_t)(q(32 * j + i) | (q(32 * j + 16 + i) << 4));
+      uint32_t v = 0;
+      for (uint32_t e = 0; e < 32; e++) v |= ((s[16 + e] >> j) & 1u) << q5_bit_pos(e);
+      for (uint32_t o = 0; o < 4; o++) dst[p.qh + ci * 4 + o] = (uint8_t)(v >> (8 * o));
+    }
+  }
+}
+
+// Q4_0: a block is one chunk whose GGUF quant bytes are already in chunk order (byte i holds
+// elements i and i + 16); d per block.
+__global__ void k_repack_q40(const uint8_t *src, uint8_t *dst, uint32_t bpr, uint32_t rows) {
+  const uint64_t nb = (uint64_t)rows * bpr, nbp = tile_rows(rows) * bpr;
+  const Q40Planes p = q40_planes(nbp);
+  for (uint64_t blk = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; blk < nb; blk += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t row = (uint32_t)(blk / bpr), b = (uint32_t)(blk % bpr);
+    const uint8_t *s = src + blk * 18;
+    const uint64_t ci = tiled(row, b, bpr);
+    dst[p.d + ci * 2] = s[0];
+    dst[p.d + ci * 2 + 1] = s[1];
+    for (uint32_t i = 0; i < 16; i++) dst[p.qs + ci * 16 + i] = s[2 + i];
+  }
+}
+
 hipError_t repack_planar(hipStream_t s, int type, const uint8_t *src, uint8_t *dst, uint32_t cols, uint32_t rows) {
   if (!rows || !cols) return hipSuccess;
-  if (!has_planar(type) || cols % block_size(type)) return hipErrorInvalidValue;
+  if (!has_planar(type, cols) || cols % block_size(type)) return hipErrorInvalidValue;
   const uint32_t bpr = cols / block_size(type);
   uint64_t grid = ((uint64_t)rows * bpr + 255) / 256;
   if (grid > 65535 * 8) grid = 65535 * 8;
   if (type == Q4_K) hipLaunchKernelGGL(k_repack_q4, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
+  else if (type == Q5_K) hipLaunchKernelGGL(k_repack_q5, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
   else if (type == Q6_K) hipLaunchKernelGGL(k_repack_q6, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
+  else if (type == Q4_0) hipLaunchKernelGGL(k_repack_q40, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
   else hipLaunchKernelGGL(k_repack_q8, dim3((uint32_t)grid), dim3(256), 0, s, src, dst, bpr, rows);
   return hipGetLastError();
 }

@@ -180,9 +180,9 @@ int wgd_upload_weights(wgd_context *ctx, int32_t type, uint32_t cols, uint32_t r
   uint64_t need = (uint64_t)rows * row_bytes(type, cols);
   if (bytes != need) return fail(ctx, WGD_E_INVALID, "wgd_upload_weights: %llu bytes given, shape needs %llu", (unsigned long long)bytes, (unsigned long long)need);
   wgd_buffer *b = nullptr;
-  int rc = wgd_buffer_create(ctx, has_planar(type) ? planar_bytes(type, cols, rows) : need, label ? label : "weights", &b);
+  int rc = wgd_buffer_create(ctx, has_planar(type, cols) ? planar_bytes(type, cols, rows) : need, label ? label : "weights", &b);
   if (rc) return rc;
-  if (has_planar(type)) {
+  if (has_planar(type, cols)) {
     void *raw = nullptr;
     rc = ctx_alloc(ctx, need, "upload staging", &raw);
     if (!rc) rc = ctx_check(ctx, hipMemcpyAsync(raw, data, need, hipMemcpyHostToDevice, ctx->stream), "wgd_upload_weights");

@@ -76,6 +76,23 @@ def q6k_blocks(rng: np.random.Generator, nb: int, std: float = 0.02) -> np.ndarr
     return b.reshape(-1)
 
 
+def q5k_blocks(rng: np.random.Generator, nb: int, std: float = 0.02) -> np.ndarray:
+    """nb random Q5_K super-blocks (176 bytes each), centred, weight std ~ ``std``."""
+    b = np.frombuffer(rng.bytes(nb * 176), np.uint8).copy().reshape(nb, 176)
+    d = (std / 480.0) * rng.uniform(0.75, 1.25, nb)
+    b[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(nb, 2)
+    b[:, 2:4] = (15.5 * d).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
+def q4_0_blocks(rng: np.random.Generator, nb: int, std: float = 0.02) -> np.ndarray:
+    """nb random Q4_0 blocks (18 bytes each), weight std ~ ``std``."""
+    b = np.frombuffer(rng.bytes(nb * 18), np.uint8).copy().reshape(nb, 18)
+    d = (std / 4.6) * rng.uniform(0.75, 1.25, nb)
+    b[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
 def q8_0_blocks(rng: np.random.Generator, nb: int, std: float = 0.02) -> np.ndarray:
     b = np.frombuffer(rng.bytes(nb * 34), np.uint8).copy().reshape(nb, 34)
     d = (std / 73.9) * rng.uniform(0.75, 1.25, nb)
