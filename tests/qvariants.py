@@ -10,6 +10,8 @@ the three shaped decoders do not use.
   one launch per matrix).
 * ``llama-q5q4``: the Q5_K_M / Q4_0 mixes of real files: Q5_K Q, K, gate, up and head,
   Q6_K V (one Q/K/V launch of two types), Q4_0 O, down and embedding table.
+* ``qwen3-f16``: every matrix F16 (the GGUF row-major layout: the F16 decode matvec and
+  the generic prompt GEMM), with Q/K norm.
 
 Dimensions are the smallest the planar K-quant kernels take: hidden 256 (Q4_K/Q6_K rows of
 whole 256-element blocks), 4 query heads x 64, 2 KV heads, FFN 512, vocab 300. Matrix blocks
@@ -20,10 +22,10 @@ from typing import List, Tuple
 import numpy as np
 
 from webgpu_amd import synth
-from webgpu_amd.gguf import F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
+from webgpu_amd.gguf import F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
 from webgpu_amd.tokenizer import byte_alphabet
 
-KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4")
+KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16")
 
 
 CHAT_SPECIALS = ["<|im_start|>", "<|im_end|>", "<|endoftext|>"]
@@ -48,32 +50,34 @@ def build(kind: str, tokenizer: bool = False):
     file also carries a byte-level BPE vocabulary with a ChatML template."""
     rng = np.random.default_rng(sum(kind.encode()) * 31 + 5)
     H, nh, nkv, hd, F, V, L = 256, 4, 2, 64, 512, 300, 2
-    arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3", "llama-q5q4": "llama"}[kind]
+    arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3", "llama-q5q4": "llama",
+            "qwen3-f16": "qwen3"}[kind]
     qd, kd = nh * hd, nkv * hd
     T: List[Tuple[str, List[int], int, np.ndarray]] = []
 
     def mat(name, cols, rows, typ, std=0.05):
         nb = rows * cols // QUANTS[typ]["block"]
         gen = {Q4_K: synth.q4k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks,
-               Q5_K: synth.q5k_blocks, Q4_0: synth.q4_0_blocks}[typ]
+               Q5_K: synth.q5k_blocks, Q4_0: synth.q4_0_blocks, F16: synth.f16_values}[typ]
         T.append((name, [cols, rows], typ, gen(rng, nb, std)))
 
     def vec(name, n, center=1.0, spread=0.1):
         v = (center + rng.uniform(-spread, spread, n)).astype(np.float32)
         T.append((name, [n], F32, v.view(np.uint8)))
 
-    q5 = kind == "llama-q5q4"
-    mat("token_embd.weight", H, V, Q4_0 if q5 else Q6_K, 0.5)
+    q5, f16 = kind == "llama-q5q4", kind == "qwen3-f16"
+    mat("token_embd.weight", H, V, Q4_0 if q5 else F16 if f16 else Q6_K, 0.5)
     vec("output_norm.weight", H)
-    mat("output.weight", H, V, Q5_K if q5 else Q6_K, 0.3)
-    k_type = Q8_0 if kind == "qwen3-mixed" else Q5_K if q5 else Q4_K
-    big, small = (Q5_K, Q4_0) if q5 else (Q4_K, Q4_K)
+    mat("output.weight", H, V, Q5_K if q5 else F16 if f16 else Q6_K, 0.3)
+    k_type = Q8_0 if kind == "qwen3-mixed" else Q5_K if q5 else F16 if f16 else Q4_K
+    big, small = (Q5_K, Q4_0) if q5 else (F16, F16) if f16 else (Q4_K, Q4_K)
+    v_type = F16 if f16 else Q6_K
     for l in range(L):
         p = f"blk.{l}."
         vec(p + "attn_norm.weight", H)
         mat(p + "attn_q.weight", H, qd, big)
         mat(p + "attn_k.weight", H, kd, k_type)
-        mat(p + "attn_v.weight", H, kd, Q6_K)
+        mat(p + "attn_v.weight", H, kd, v_type)
         mat(p + "attn_output.weight", qd, H, small)
         if kind in ("qwen2-bias", "llama-partial"):
             vec(p + "attn_q.bias", qd, 0.0, 0.2)
@@ -81,7 +85,7 @@ def build(kind: str, tokenizer: bool = False):
             vec(p + "attn_v.bias", kd, 0.0, 0.2)
         if kind == "llama-partial":
             vec(p + "attn_output.bias", H, 0.0, 0.1)
-        if kind == "qwen3-mixed":
+        if kind in ("qwen3-mixed", "qwen3-f16"):
             vec(p + "attn_q_norm.weight", hd)
             vec(p + "attn_k_norm.weight", hd)
         vec(p + "ffn_norm.weight", H)

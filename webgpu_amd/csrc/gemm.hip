@@ -141,6 +141,17 @@ __device__ __forceinline__ void load_a8(const GemmArgs &a, uint32_t row, uint32_
     return;
   }
   const uint8_t *r = a.w + (uint64_t)row * a.rb;
+  if (a.type == F16 && (a.rb & 15) == 0) {
+    // eight halves in one 16-byte load (rows stay 16-byte aligned for K % 8 == 0)
+    const uint4 v = *(const uint4 *)(r + 2 * (uint64_t)k);
+    const uint32_t h[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o[2 * i] = half_bits(h[i] & 0xFFFFu);
+      o[2 * i + 1] = half_bits(h[i] >> 16);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 8; i++) o[i] = deq_elem(a.type, r, k + i);
 }

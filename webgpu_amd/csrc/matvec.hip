@@ -530,6 +530,108 @@ __global__ __launch_bounds__(1024) void k_mv(MV m) {
   else mv_tile<T1, DU, GLU>(m, g, t, lds);
 }
 
+// ------------------------------------------------------------------ F16 weights
+//
+// F16 matrices keep the GGUF row-major layout (a row is K contiguous halves, 16-byte
+// aligned for K % 8 == 0) and take the same QX activation, epilogues and launch groups as the
+// integer kernel. A workgroup of four wavefronts owns RT rows (RT / 4 per wavefront, four at a
+// time): the activation is rebuilt in LDS as f32 from its digits (the exact integer
+// d0 * 254^2 + d1 * 254 + d2 times scale / 254^2, as the integer kernel combines them), each
+// lane reads 8 halves of each of four rows per step (a wavefront reads 1 KB of a row), and
+// multiplies them in f32 with the activation (the reference's arithmetic, shaders.ts:39-54);
+// the row sums are reduced across the wavefront and finished by the epilogue threads.
+constexpr uint32_t MV16_THREADS = 256;
+
+__device__ __forceinline__ float dot8_f16(const uint4 &w, const float4 &a, const float4 &b) {
+  float s = f16lo(w.x) * a.x;
+  s = fmaf(f16hi(w.x), a.y, s);
+  s = fmaf(f16lo(w.y), a.z, s);
+  s = fmaf(f16hi(w.y), a.w, s);
+  s = fmaf(f16lo(w.z), b.x, s);
+  s = fmaf(f16hi(w.z), b.y, s);
+  s = fmaf(f16lo(w.w), b.z, s);
+  return fmaf(f16hi(w.w), b.w, s);
+}
+
+template <bool GLU>
+__global__ __launch_bounds__(MV16_THREADS) void k_mv16(MV m) {
+  extern __shared__ __attribute__((aligned(16))) float l16[];
+  uint32_t t = blockIdx.x;
+  MVSeg g = m.seg[0];
+  if (m.nseg > 1 && t >= m.seg[0].tiles) {
+    t -= m.seg[0].tiles;
+    g = m.seg[1];
+    if (m.nseg > 2 && t >= m.seg[1].tiles) { t -= m.seg[1].tiles; g = m.seg[2]; }
+  }
+  const uint32_t K = m.x.len, RT = m.RT, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  float *xs = l16, *vals = xs + K, *vals1 = vals + RT, *red = vals1 + RT;
+  const uint32_t row0 = t * RT;
+  const RowIn rin = row_inputs(m, g, row0 + tid);  // used by threads tid < RT
+  // the activation, four elements per thread and step (K % 16 == 0)
+  for (uint32_t i = 4 * tid; i < K; i += 4 * MV16_THREADS) {
+    const uint32_t d0 = *(const uint32_t *)(m.x.d[0] + i), d1 = *(const uint32_t *)(m.x.d[1] + i);
+    const uint32_t d2 = *(const uint32_t *)(m.x.d[2] + i);
+    const float sc = m.x.scale[i >> 4] * (1.f / 64516.f);
+    float4 v;
+    float *pv = &v.x;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int a = (int8_t)(d0 >> (8 * e)), b = (int8_t)(d1 >> (8 * e)), c = (int8_t)(d2 >> (8 * e));
+      pv[e] = (float)(a * 64516 + b * 254 + c) * sc;
+    }
+    *(float4 *)(xs + i) = v;
+  }
+  if (m.x.normed) {
+    float ss = 0.f;
+    for (uint32_t b = tid; b < K / 16; b += MV16_THREADS) ss += m.x.sq[b];
+    ss = wave_sum(ss);
+    if (lane == 0) red[wv] = ss;
+  }
+  __syncthreads();
+  const Rsrc rw = make_rsrc(g.w, g.bytes), rw1 = make_rsrc(GLU ? g.w1 : g.w, g.bytes);
+  const uint32_t per = RT / 4;
+  for (uint32_t r0 = wv * per; r0 < (wv + 1) * per; r0 += 4) {
+    float a[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (uint32_t k = lane * 8; k < K; k += 512) {
+      uint4 wq[4], wq1[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        // rows past the matrix read zero (offsets past the buffer range)
+        const uint32_t off = ((row0 + r0 + j) * K + k) * 2;
+        wq[j] = bl16(rw, off, 0);
+        if (GLU) wq1[j] = bl16(rw1, off, 0);
+      }
+      const float4 x0 = *(const float4 *)(xs + k), x1 = *(const float4 *)(xs + k + 4);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        a[j] += dot8_f16(wq[j], x0, x1);
+        if (GLU) a1[j] += dot8_f16(wq1[j], x0, x1);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float v = wave_sum(a[j]);
+      const float v1 = GLU ? wave_sum(a1[j]) : 0.f;
+      if (lane == 0) {
+        vals[r0 + j] = v;
+        if (GLU) vals1[r0 + j] = v1;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid >= ((RT + 63) & ~63u)) return;
+  float xm = 1.f;
+  if (m.x.normed) xm = 1.f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + m.x.eps);
+  const bool inside = tid < RT && row0 + tid < g.rows;
+  const float v = tid < RT ? vals[tid] : 0.f, v1 = (GLU && tid < RT) ? vals1[tid] : 0.f;
+  const float out = finish_row(m, g, row0 + tid, inside, v * xm, v1 * xm, rin);
+  if (m.arg_part) {
+    const uint64_t k = wave_max_key(inside ? arg_key(out, row0 + tid) : 0);
+    if ((tid & 63) == 0) m.arg_part[blockIdx.x * ((RT + 63) >> 6) + (tid >> 6)] = k;
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 uint64_t qx_bytes(uint32_t K) {
@@ -562,7 +664,31 @@ hipError_t quantize(hipStream_t s, const float *x, uint32_t K, const float *norm
   return hipGetLastError();
 }
 
+// F16 rows of up to 32768 halves (the f32 activation fits in LDS), 32-bit buffer offsets.
+static bool mv16_supported(const Matrix &w) {
+  return w.type == F16 && w.layout == LAYOUT_GGUF && w.cols && w.rows && w.cols % 16 == 0 && w.cols <= 32768 &&
+         ((uint64_t)w.rows + 64) * w.cols * 2 < (1ull << 31);
+}
+
+// Row tiles of 64, 32 or 16 rows: the largest that still gives every CU a workgroup.
+static MVPlan mv16_plan(const Matrix &w, const uint32_t *rows, uint32_t n) {
+  const uint32_t cus = (uint32_t)device_cu_count();
+  MVPlan p{};
+  for (uint32_t rt = 64; rt >= 16; rt /= 2) {
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < n; i++) tiles += (rows[i] + rt - 1) / rt;
+    p.RT = rt;
+    p.tiles = tiles;
+    if (tiles >= cus) break;
+  }
+  p.C = w.cols; p.NS = p.NSB = p.NR = p.ITER = p.DU = 1;
+  p.threads = MV16_THREADS;
+  p.lds = 4 * (w.cols + 2 * p.RT + 4);
+  return p;
+}
+
 bool mv_supported(const Matrix &w) {
+  if (w.type == F16) return mv16_supported(w);
   if (w.layout != LAYOUT_PLANAR || !w.cols || !w.rows) return false;
   if (w.type == Q4_K || w.type == Q5_K || w.type == Q6_K) return w.cols % 256 == 0;
   if (w.type == Q8_0 || w.type == Q4_0) return w.cols % 32 == 0;
@@ -589,6 +715,7 @@ uint32_t mv_arg_entries(const Matrix &w) {
 // only queues), when the activation staging is amortised over few rows, and for idle chunk
 // columns.
 MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out) {
+  if (w.type == F16) return mv16_plan(w, rows, n);
   MVPlan best_p{};
   const uint32_t N = chunk_elems(w.type), C = w.cols / N, CQ = (C + 7) / 8;
   const uint32_t cus = (uint32_t)device_cu_count();
@@ -676,6 +803,44 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   if ((epi == MV_SILU || epi == MV_GELU) != glu) return hipErrorInvalidValue;
   if (x.len != w0.cols) return hipErrorInvalidValue;
   uint32_t rows[MV_MAX_SEGS];
+  if (w0.type == F16) {
+    for (uint32_t i = 0; i < n; i++) {
+      const Matrix &w = *t[i].w;
+      if (!mv16_supported(w) || w.cols != w0.cols || !t[i].y || (t[i].w1 != nullptr) != glu) return hipErrorInvalidValue;
+      if (glu && (t[i].w1->type != F16 || t[i].w1->layout != w.layout || t[i].w1->cols != w.cols ||
+                  t[i].w1->rows != w.rows))
+        return hipErrorInvalidValue;
+      rows[i] = w.rows;
+    }
+    const MVPlan p = mv16_plan(w0, rows, n);
+    if (p.lds > lds_limit()) return hipErrorInvalidValue;
+    MV m{};
+    m.nseg = n;
+    for (uint32_t i = 0; i < n; i++) {
+      MVSeg &g = m.seg[i];
+      g.w = t[i].w->data; g.w1 = glu ? t[i].w1->data : nullptr;
+      g.bytes = (uint32_t)((uint64_t)rows[i] * w0.cols * 2);
+      g.y = t[i].y; g.bias = t[i].bias; g.rows = rows[i];
+      g.tiles = (rows[i] + p.RT - 1) / p.RT;
+    }
+    m.x = x; m.C = w0.cols; m.ke = w0.cols; m.RT = p.RT; m.NS = m.NSB = m.NR = m.ITER = m.U = 1;
+    m.epi = epi;
+    if (qout) { m.oq = out->q; m.oq_norm = out->norm_w; }
+    if (out && out->arg_part) {
+      if (n != 1) return hipErrorInvalidValue;
+      m.arg_part = out->arg_part;
+    }
+    auto go = [&](auto kernel) -> hipError_t {
+      static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
+      if (p.lds > 64 * 1024 && !big) {
+        (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit());
+        big = true;
+      }
+      hipLaunchKernelGGL(kernel, dim3(p.tiles), dim3(MV16_THREADS), p.lds, s, m);
+      return hipGetLastError();
+    };
+    return glu ? go(k_mv16<true>) : go(k_mv16<false>);
+  }
   // Q6_K segments may share a launch with Q4_K or Q5_K ones (same chunk shape); other
   // types run alone
   int other = -1;

@@ -93,6 +93,11 @@ def q4_0_blocks(rng: np.random.Generator, nb: int, std: float = 0.02) -> np.ndar
     return b.reshape(-1)
 
 
+def f16_values(rng: np.random.Generator, n: int, std: float = 0.02) -> np.ndarray:
+    """n normal F16 weights of standard deviation ``std``, as bytes."""
+    return (rng.standard_normal(n) * std).astype(np.float16).view(np.uint8).copy()
+
+
 def q8_0_blocks(rng: np.random.Generator, nb: int, std: float = 0.02) -> np.ndarray:
     b = np.frombuffer(rng.bytes(nb * 34), np.uint8).copy().reshape(nb, 34)
     d = (std / 73.9) * rng.uniform(0.75, 1.25, nb)
