@@ -162,6 +162,13 @@ int wgd_activate(wgd_context *ctx, wgd_buffer *x, uint32_t n);
  * WGD_E_NONFINITE when no entry is finite. */
 int wgd_argmax(wgd_context *ctx, const wgd_buffer *logits, uint32_t n, wgd_buffer *out,
                int32_t *host_index);
+/* sample (engine.ts:305-324) on the device for logits[0..n): the first finite maximum
+ * when temperature is 0, else the top_k finite logits (ties to the lower index),
+ * exp((l - best) / T) in f64, the top_p prefix and a draw with the index-th output of
+ * splitmix64(seed) as Math.random(). Waits; returns the token (WGD_E_NONFINITE when no
+ * logit is finite, WGD_E_INVALID for settings the reference rejects). */
+int wgd_sample(wgd_context *ctx, const wgd_buffer *logits, uint32_t n, double temperature, uint32_t top_k,
+               double top_p, uint64_t seed, uint32_t index, int32_t *token);
 /* Embedding gather of `forward` (engine.ts:140-145) on the device:
  * out[b*hidden + i] = f32(deq(table)[ids[b]*hidden + i] * scale) with the product taken
  * in f64 (scale = sqrt(hidden) for Gemma 3, else 1). ids is int32[n]. */
@@ -201,7 +208,8 @@ int wgd_model_tensor(wgd_model *m, const char *name, int32_t type, int32_t n_dim
 int wgd_model_ready(wgd_model *m);
 /* PagedEngine.forward (engine.ts:138-180) for ids[0..n) at positions start..start+n-1
  * (n <= batch). When logits or argmax is non-NULL the last row's logits are produced
- * (vocab f32 copied to `logits`; greedy id to `argmax`, WGD_E_NONFINITE if none). */
+ * (vocab f32 copied to `logits`; the next token to `argmax`, WGD_E_NONFINITE if no logit
+ * is finite: the greedy id, or with sampling set the draw for position start + n). */
 int wgd_model_forward(wgd_model *m, const int32_t *ids, int32_t n, int32_t start,
                       float *logits, int32_t *argmax);
 /* The greedy decode loop of generate (engine.ts:290-298) kept on the device: for
@@ -210,6 +218,12 @@ int wgd_model_forward(wgd_model *m, const int32_t *ids, int32_t n, int32_t start
  * captured HIP graph; positions and ids never leave the device between steps. */
 int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count,
                      int32_t *out_tokens);
+/* The token pick of generate (engine.ts:261-264, 292, 305-324) for wgd_model_forward and
+ * wgd_model_decode: temperature 0 is greedy; otherwise top_k / top_p sampling on the
+ * device, where Math.random() becomes the p-th output of splitmix64(seed) for the token
+ * at position p (the same tokens whether decoded eagerly, in chunks or by graph replay).
+ * Validated as the reference validates GenerationOptions (WGD_E_INVALID). */
+int wgd_model_sampling(wgd_model *m, double temperature, uint32_t top_k, double top_p, uint64_t seed);
 void wgd_model_destroy(wgd_model *m);
 
 #ifdef __cplusplus

@@ -116,6 +116,59 @@ def argmax(logits: np.ndarray) -> int:
     return int(lib().orc_argmax(_ptr(a), a.size))
 
 
+MASK64 = (1 << 64) - 1
+
+
+def splitmix64_at(seed: int, index: int) -> int:
+    """The index-th output (from 0) of splitmix64 seeded with ``seed`` (Steele, Lea and
+    Flood, OOPSLA 2014): the generator whose uniforms stand in for Math.random()."""
+    z = (seed + (index + 1) * 0x9E3779B97F4A7C15) & MASK64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & MASK64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & MASK64
+    return z ^ (z >> 31)
+
+
+def uniform(seed: int, index: int) -> float:
+    """The 53-bit uniform in [0, 1) drawn for the token at position ``index``."""
+    return (splitmix64_at(seed, index) >> 11) * 2.0 ** -53
+
+
+def sample(logits, temperature: float, top_k: int, top_p: float, u: float) -> int:
+    """sample() of src/core/engine.ts:305-324 with Math.random() = u.
+
+    Best finite logit (first index of the maximum); temperature 0 returns it. Otherwise the
+    top_k finite logits in descending order with ties to the lower index (the order the
+    reference's insertion into a stably sorted list leaves, :312-315), f64 probabilities
+    exp((l - best) / T) (:314), their sum (:317), the prefix whose share reaches top_p
+    (:318-319) and the draw u * retained walked down it (:320-322)."""
+    l = np.asarray(logits, np.float32)
+    idx = np.flatnonzero(np.isfinite(l))
+    if idx.size == 0:
+        raise ValueError("Inference produced non-finite logits.")
+    vals = l[idx]
+    best_id = int(idx[int(np.argmax(vals))])
+    best = float(l[best_id])
+    if temperature == 0:
+        return best_id
+    cand = idx[np.argsort(-vals.astype(np.float64), kind="stable")[:top_k]]
+    probs = [math.exp((float(l[i]) - best) / temperature) for i in cand]
+    total = 0.0
+    for p in probs:
+        total += p
+    retained, cutoff = 0.0, 0
+    while cutoff < len(probs):
+        retained += probs[cutoff]
+        cutoff += 1
+        if retained / total >= top_p:
+            break
+    draw = u * retained
+    for i in range(cutoff):
+        draw -= probs[i]
+        if draw <= 0:
+            return int(cand[i])
+    return best_id
+
+
 def threads() -> int:
     return int(lib().orc_threads())
 

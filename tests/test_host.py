@@ -203,8 +203,9 @@ def test_token_loop_runs_to_the_exact_context_boundary():
         return [0] * count
     eng.forward, eng.forward_argmax, eng.decode = fwd, fwd_argmax, decode
     eng.stats = lambda: {}
+    eng.set_sampling = lambda *a: None
     count = 0
-    for ev in eng.generate([0] * 1000, GenerationOptions(maxTokens=32768)):
+    for ev in eng.generate([0] * 1000, GenerationOptions(temperature=0, maxTokens=32768)):
         count += 1
         assert ev.promptTokens == 1000 and ev.contextLength == 4096
     assert count == 3096 and max(positions) == 4094
@@ -223,6 +224,7 @@ def _scripted_engine(context, batch, caps):
         return [7] * count
     eng.decode = decode
     eng.stats = lambda: {}
+    eng.set_sampling = lambda *a: None
     return eng, counts
 
 
@@ -230,10 +232,10 @@ def test_device_chunks_stay_within_the_sliding_ring_slack():
     # a ring of window + batch - 1 slots survives at most `batch` positions written past
     # the cached prefix, so a model with one decodes at most `batch` tokens per chunk
     eng, counts = _scripted_engine(256, 8, [31, 256])
-    assert len(list(eng.generate([1, 2, 3], GenerationOptions(maxTokens=100)))) == 100
+    assert len(list(eng.generate([1, 2, 3], GenerationOptions(temperature=0, maxTokens=100)))) == 100
     assert max(counts) == 8
     eng, counts = _scripted_engine(256, 8, [256, 256])
-    list(eng.generate([1, 2, 3], GenerationOptions(maxTokens=100)))
+    list(eng.generate([1, 2, 3], GenerationOptions(temperature=0, maxTokens=100)))
     assert max(counts) == 32
 
 
@@ -243,7 +245,7 @@ def test_abort_signal_stops_generation_and_drops_the_prefix():
     sig = AbortSignal()
     got = []
     with pytest.raises(AbortError, match="Stopped by user"):
-        for ev in eng.generate([1, 2, 3], GenerationOptions(maxTokens=50), signal=sig):
+        for ev in eng.generate([1, 2, 3], GenerationOptions(temperature=0, maxTokens=50), signal=sig):
             got.append(ev.token)
             if len(got) == 3:
                 sig.abort()
@@ -257,14 +259,14 @@ def test_generation_options_are_validated_like_the_reference():
         with pytest.raises(ValueError, match="Invalid sampling settings"):
             eng.generate([1], GenerationOptions(**bad))
     with pytest.raises(ValueError, match="maxTokens"):
-        eng.generate([1], GenerationOptions(maxTokens=0))
+        eng.generate([1], GenerationOptions(temperature=0, maxTokens=0))
 
 
 def test_an_unstarted_generation_leaves_the_engine_free():
     eng, _ = _scripted_engine(512, 16, [512])
-    eng.generate([1, 2], GenerationOptions(maxTokens=4))   # never iterated
+    eng.generate([1, 2], GenerationOptions(temperature=0, maxTokens=4))   # never iterated
     assert not eng.busy
-    assert len(list(eng.generate([1, 2], GenerationOptions(maxTokens=4)))) == 4
+    assert len(list(eng.generate([1, 2], GenerationOptions(temperature=0, maxTokens=4)))) == 4
 
 
 def test_load_options_follow_the_performance_presets():

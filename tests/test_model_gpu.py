@@ -74,7 +74,7 @@ def test_tiny_check_dense_tokens_and_logits():
     eng, ora, ids, toks = check_model("tiny", 8, 4)
     try:
         # The same tokens through the public token loop (prefill + on-device greedy decode).
-        events = list(eng.generate(ids, GenerationOptions(maxTokens=4)))
+        events = list(eng.generate(ids, GenerationOptions(temperature=0, maxTokens=4)))
         assert [e.token for e in events] == toks
         assert [e.tokens for e in events] == [1, 2, 3, 4] and all(e.promptTokens == 8 for e in events)
         assert eng.tokensInCache == ids + toks[:3]
@@ -103,12 +103,12 @@ def test_prefix_reuse_across_turns():
     f, g, c, caps, eng = build("tiny", 512, batch=8)
     try:
         ids = synth.prompt_ids(c.vocab, 20, 5)
-        a = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=6))]
+        a = [e.token for e in eng.generate(ids, GenerationOptions(temperature=0, maxTokens=6))]
         # A second turn that extends the cached conversation reuses its prefix.
         follow = ids + a[:5] + [1, 2, 3]
-        b = [e.token for e in eng.generate(follow, GenerationOptions(maxTokens=5))]
+        b = [e.token for e in eng.generate(follow, GenerationOptions(temperature=0, maxTokens=5))]
         eng.reset()
-        c2 = [e.token for e in eng.generate(follow, GenerationOptions(maxTokens=5))]
+        c2 = [e.token for e in eng.generate(follow, GenerationOptions(temperature=0, maxTokens=5))]
         assert b == c2
     finally:
         eng.dispose()

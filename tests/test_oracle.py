@@ -279,3 +279,75 @@ def test_model_variants_match_independent_forward(variant):
     logits = m.forward(ids[8:], 8)
     ref = npref.forward(f, g, c, ids)
     np.testing.assert_allclose(logits, ref, rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------- sampling (engine.ts:305-324)
+def _insertion_sample(logits, temperature, top_k, top_p, u):
+    """The reference's own steps, literally: a candidate list kept stably sorted by value
+    while scanning (engine.ts:310-316). Checks the oracle's stable-argsort selection."""
+    best, best_id = -math.inf, -1
+    for i, v in enumerate(logits):
+        if math.isfinite(v) and v > best:
+            best, best_id = float(v), i
+    if temperature == 0:
+        return best_id
+    cand = []
+    for i, v in enumerate(logits):
+        if not math.isfinite(v):
+            continue
+        if len(cand) < top_k or v > cand[-1][1]:
+            cand.append((i, float(v), math.exp((float(v) - best) / temperature)))
+            cand.sort(key=lambda c: -c[1])
+            if len(cand) > top_k:
+                cand.pop()
+    total = sum(c[2] for c in cand)
+    retained, cutoff = 0.0, 0
+    while cutoff < len(cand):
+        retained += cand[cutoff][2]
+        cutoff += 1
+        if retained / total >= top_p:
+            break
+    draw = u * retained
+    for c in cand[:cutoff]:
+        draw -= c[2]
+        if draw <= 0:
+            return c[0]
+    return best_id
+
+
+def test_splitmix64_known_answer():
+    # the first output of splitmix64 seeded with 0 (the published generator's first value)
+    assert orc.splitmix64_at(0, 0) == 0xE220A8397B1DCDAF
+    # index i is the (i+1)-th step of one generator: consecutive states differ by the gamma
+    assert orc.splitmix64_at(0x9E3779B97F4A7C15, 0) == orc.splitmix64_at(0, 1)
+    us = [orc.uniform(7, i) for i in range(20000)]
+    assert 0.0 <= min(us) and max(us) < 1.0 and abs(np.mean(us) - 0.5) < 0.01
+
+
+def test_sample_matches_the_reference_steps_with_ties_and_non_finite_logits():
+    rng = np.random.default_rng(5)
+    for trial in range(300):
+        n = int(rng.integers(1, 60))
+        l = np.round(rng.standard_normal(n) * 2, int(rng.integers(0, 2))).astype(np.float32)  # many ties
+        if trial % 5 == 0:
+            l[rng.integers(0, n, 3)] = [np.inf, -np.inf, np.nan]
+        if not np.isfinite(l).any():
+            continue
+        t = float(rng.choice([0.0, 0.3, 0.7, 1.5, 2.0]))
+        k, p, u = int(rng.integers(1, 12)), float(rng.choice([0.05, 0.5, 0.9, 1.0])), float(rng.random())
+        assert orc.sample(l, t, k, p, u) == _insertion_sample(l, t, k, p, u), (trial, l, t, k, p, u)
+
+
+def test_sample_closed_forms():
+    l = np.array([1.0, 3.0, 3.0, -2.0, 0.5], np.float32)
+    assert orc.sample(l, 0.0, 40, 0.9, 0.99) == 1           # greedy: first index of the maximum
+    for u in (0.0, 0.3, 0.999):
+        assert orc.sample(l, 0.7, 1, 1.0, u) == 1           # top-1 is the best
+        assert orc.sample(l, 0.7, 40, 1e-9, u) == 1         # a tiny top-p keeps one
+    # frequencies over a fine grid of u are the retained probabilities, normalised
+    probs = np.exp((np.array([3.0, 3.0, 1.0, 0.5, -2.0]) - 3.0) / 0.7)
+    grid = (np.arange(20000) + 0.5) / 20000
+    got = np.bincount([orc.sample(l, 0.7, 40, 1.0, u) for u in grid], minlength=5)[[1, 2, 0, 4, 3]] / grid.size
+    assert np.abs(got - probs / probs.sum()).max() < 2e-4
+    with pytest.raises(ValueError):
+        orc.sample(np.array([np.nan, np.inf], np.float32), 0.7, 40, 0.9, 0.5)

@@ -92,7 +92,7 @@ def test_generate_from_chat_messages():
         assert tok is not None and tok.style == "chatml"
         messages = [{"role": "user", "content": "hello world, user"}]
         ids = tok.chat(messages)
-        events = list(eng.generate(messages, GenerationOptions(maxTokens=8)))
+        events = list(eng.generate(messages, GenerationOptions(temperature=0, maxTokens=8)))
         want, logits, pos = [], ora.forward(ids, 0), len(ids)
         for _ in range(8):
             t = int(np.argmax(logits))
@@ -122,16 +122,16 @@ def test_sliding_ring_survives_a_turn_that_ends_inside_a_device_chunk():
         assert max(eng.kvCapacities) == 31
         ids = synth.prompt_ids(c.vocab, 30, seed=21)
         free = SimpleNamespace(eos=set(), decode=lambda t: "")
-        gen = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=12), tokenizer=free)]
+        gen = [e.token for e in eng.generate(ids, GenerationOptions(temperature=0, maxTokens=12), tokenizer=free)]
         stop = gen[2]
         turn = SimpleNamespace(eos={stop}, decode=lambda t: "")
         eng.reset()
-        first = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=40), tokenizer=turn)]
+        first = [e.token for e in eng.generate(ids, GenerationOptions(temperature=0, maxTokens=40), tokenizer=turn)]
         assert first == gen[:gen.index(stop)]
         follow = ids + first + [stop, 5, 6, 7, 8]
-        cached = [e.token for e in eng.generate(follow, GenerationOptions(maxTokens=20), tokenizer=free)]
+        cached = [e.token for e in eng.generate(follow, GenerationOptions(temperature=0, maxTokens=20), tokenizer=free)]
         eng.reset()
-        fresh = [e.token for e in eng.generate(follow, GenerationOptions(maxTokens=20), tokenizer=free)]
+        fresh = [e.token for e in eng.generate(follow, GenerationOptions(temperature=0, maxTokens=20), tokenizer=free)]
         assert cached == fresh
     finally:
         eng.dispose()
@@ -149,14 +149,14 @@ def test_runtime_api_drives_the_engine_on_its_worker_thread():
         info = rt.load(f, LoadOptions(contextLength=256, performance="fast"))
         assert info.batchSize == 128 and info.performance == "fast" and info.fileBytes == f.size
         turn1 = [{"role": "user", "content": "hello world"}]
-        a = list(rt.generate(turn1, GenerationOptions(maxTokens=6)))
+        a = list(rt.generate(turn1, GenerationOptions(temperature=0, maxTokens=6)))
         turn2 = turn1 + [{"role": "assistant", "content": a[-1].text if a else ""},
                          {"role": "user", "content": "hello user"}]
-        b = [e.token for e in rt.generate(turn2, GenerationOptions(maxTokens=6))]
+        b = [e.token for e in rt.generate(turn2, GenerationOptions(temperature=0, maxTokens=6))]
         ref.load(f, LoadOptions(contextLength=256, batchSize=128))
-        assert [e.token for e in a] == [e.token for e in ref.generate(turn1, GenerationOptions(maxTokens=6))]
-        assert b == [e.token for e in ref.generate(turn2, GenerationOptions(maxTokens=6))]
-        it = rt.generate(turn1, GenerationOptions(maxTokens=200))
+        assert [e.token for e in a] == [e.token for e in ref.generate(turn1, GenerationOptions(temperature=0, maxTokens=6))]
+        assert b == [e.token for e in ref.generate(turn2, GenerationOptions(temperature=0, maxTokens=6))]
+        it = rt.generate(turn1, GenerationOptions(temperature=0, maxTokens=200))
         next(it, None)
         rt.stop()
         try:

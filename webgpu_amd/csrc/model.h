@@ -27,6 +27,7 @@ struct wgd_context {
   uint64_t gemm_part_floats = 0;
   uint16_t *gemm_xs = nullptr;        // its input split into bf16 (hi, lo)
   uint64_t gemm_xs_elems = 0;
+  wgd::SampleParams *sample_params = nullptr;  // settings of wgd_sample
 };
 
 namespace wgd {

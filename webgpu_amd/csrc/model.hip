@@ -38,7 +38,6 @@ struct Layer {
   uint32_t cap = 0;
 };
 
-struct StepState { int32_t pos, token, step, error; };
 
 enum Slot { S_ATTN_NORM, S_Q, S_K, S_V, S_O, S_QB, S_KB, S_VB, S_OB, S_QN, S_KN, S_POST_ATTN, S_FFN_NORM,
             S_GATE, S_UP, S_DOWN, S_POST_FFW, S_COUNT };
@@ -79,6 +78,11 @@ struct wgd_model {
   float2 *rope_batch[2] = {nullptr, nullptr};  // a prompt batch's rotations (rope_table)
   void *qx_attn = nullptr, *qx_ffn = nullptr, *qx_o = nullptr, *qx_down = nullptr, *qx_head = nullptr;
   hipGraph_t graph = nullptr;
+  // the sampling variant of the decode step (its own graph); settings in device memory
+  bool sampling = false;
+  SampleParams *sample_params = nullptr;
+  hipGraph_t graph_s = nullptr;
+  hipGraphExec_t exec_s = nullptr;
   hipGraphExec_t exec = nullptr;
   std::vector<void *> owned;
 };
@@ -467,6 +471,9 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
   MVOut hout;
   hout.arg_part = m->arg_part;
   WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H, true, c.epsilon), m->logits, MV_STORE, &hout));
+  if (m->sampling)
+    return sample(s, m->logits, c.vocab, m->sample_params, -1, m->state, m->argmax_buf, m->tokens,
+                  (uint32_t)c.context, advance);
   hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(256), 0, s, (const uint64_t *)m->arg_part, m->arg_entries,
                      m->argmax_buf, m->state, m->tokens, (uint32_t)m->c.context, advance ? 1 : 0);
   return hipGetLastError();
@@ -479,6 +486,9 @@ hipError_t decode_step_generic(wgd_model *m, bool advance) {
   WGD_HIP(embed_matrix(s, m->embd, &m->state->token, m->hidden, 1, m->c.embed_scale));
   WGD_HIP(layers_batched(m, 1, 0, &m->state->pos));
   WGD_HIP(head(m, 0));
+  if (m->sampling)
+    return sample(s, m->logits, m->c.vocab, m->sample_params, -1, m->state, m->argmax_buf, m->tokens,
+                  (uint32_t)m->c.context, advance);
   if (advance) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, m->state, (const int32_t *)m->argmax_buf, m->tokens,
                        (uint32_t)m->c.context);
@@ -510,6 +520,8 @@ void wgd::model_destroy(wgd_model *m) {
   hipStreamSynchronize(ctx->stream);
   if (m->exec) hipGraphExecDestroy(m->exec);
   if (m->graph) hipGraphDestroy(m->graph);
+  if (m->exec_s) hipGraphExecDestroy(m->exec_s);
+  if (m->graph_s) hipGraphDestroy(m->graph_s);
   for (void *p : m->owned) ctx_free(ctx, p);
   ctx->models.erase(m);
   delete m;
@@ -555,6 +567,7 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
   rc = rc ? rc : alloc_t(m, 1, "step state", &m->state);
   rc = rc ? rc : alloc_t(m, (uint64_t)c.context + 1, "decode tokens", &m->tokens);
   rc = rc ? rc : alloc_t(m, 2 + 2 * 256, "argmax", &m->argmax_buf);
+  rc = rc ? rc : alloc_t(m, 1, "sampling settings", &m->sample_params);
   m->att_part_floats = attention_scratch_floats(c.heads, c.head_dim, 1, (uint32_t)device_cu_count() * 4);
   if (decode_attention_supported(c.heads, c.kv_heads, c.head_dim))
     for (int l = 0; l < c.layers; l++)
@@ -807,6 +820,10 @@ int wgd_model_forward(wgd_model *m, const int32_t *ids, int32_t n, int32_t start
     if (!rc) rc = ctx_check(ctx, embed_matrix(s, m->embd, m->ids, m->hidden, n, m->c.embed_scale), "embed");
     if (!rc) rc = ctx_check(ctx, layers_batched(m, (uint32_t)n, (uint32_t)start), "forward");
     if (!rc && want) rc = ctx_check(ctx, head(m, (uint32_t)n - 1), "head");
+    // the next token takes position start + n
+    if (!rc && want && m->sampling)
+      rc = ctx_check(ctx, sample(s, m->logits, m->c.vocab, m->sample_params, start + n, nullptr, m->argmax_buf, nullptr, 0,
+                                 false), "sample");
   }
   if (!rc) rc = ctx_sync(ctx, "GPU fault during forward");
   if (rc) return rc;
@@ -838,11 +855,13 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count, 
   StepState st = {start, token, 0, 0};
   rc = ctx_check(ctx, hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s), "decode");
   if (rc) return rc;
+  hipGraph_t &graph = m->sampling ? m->graph_s : m->graph;
+  hipGraphExec_t &exec = m->sampling ? m->exec_s : m->exec;
   if (!m->use_graph) {
     // Eager launches (WGD_GRAPH=0): same kernels, one host launch each; used under tracers.
     for (int32_t i = 0; i < count && !rc; i++) rc = ctx_check(ctx, decode_step(m, true), "decode");
     if (rc) return rc;
-  } else if (!m->exec) {
+  } else if (!exec) {
     // Run one step eagerly first: it validates every launch outside capture.
     rc = ctx_check(ctx, decode_step(m, true), "decode");
     if (!rc) rc = ctx_sync(ctx, "GPU fault during decode");
@@ -853,16 +872,16 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count, 
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(s, &g);
     if (e != hipSuccess || e2 != hipSuccess) { if (g) hipGraphDestroy(g); return hip_fail(ctx, e != hipSuccess ? e : e2, "graph capture"); }
-    m->graph = g;
-    e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
-    if (e != hipSuccess) { m->exec = nullptr; return hip_fail(ctx, e, "graph instantiate"); }
+    graph = g;
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) { exec = nullptr; return hip_fail(ctx, e, "graph instantiate"); }
     for (int32_t i = 1; i < count; i++) {
-      e = hipGraphLaunch(m->exec, s);
+      e = hipGraphLaunch(exec, s);
       if (e != hipSuccess) return hip_fail(ctx, e, "graph launch");
     }
   } else {
     for (int32_t i = 0; i < count; i++) {
-      hipError_t e = hipGraphLaunch(m->exec, s);
+      hipError_t e = hipGraphLaunch(exec, s);
       if (e != hipSuccess) return hip_fail(ctx, e, "graph launch");
     }
   }
@@ -874,6 +893,22 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count, 
   e = hipMemcpy(out_tokens, m->tokens, sizeof(int32_t) * count, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(ctx, e, "decode tokens");
   if (fin.error) return fail(ctx, WGD_E_NONFINITE, "Inference produced non-finite logits. Stop and report this model/runtime combination.");
+  return WGD_OK;
+}
+
+int wgd_model_sampling(wgd_model *m, double temperature, uint32_t top_k, double top_p, uint64_t seed) {
+  if (!m) return fail(nullptr, WGD_E_INVALID, "wgd_model_sampling: NULL model");
+  wgd_context *ctx = m->ctx;
+  hipSetDevice(ctx->device);
+  // engine.ts:262-264
+  if (!(temperature >= 0.0 && temperature <= 2.0) || top_k < 1 || top_k > 200 || !(top_p > 0.0 && top_p <= 1.0))
+    return fail(ctx, WGD_E_INVALID, "Invalid sampling settings.");
+  const SampleParams p = {temperature, top_p, top_k, 0, seed};
+  hipError_t e = hipMemcpyAsync(m->sample_params, &p, sizeof p, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sampling settings");
+  int rc = ctx_sync(ctx, "sampling settings");
+  if (rc) return rc;
+  m->sampling = temperature != 0.0;
   return WGD_OK;
 }
 

@@ -464,6 +464,31 @@ int wgd_argmax(wgd_context *ctx, const wgd_buffer *logits, uint32_t n, wgd_buffe
   return WGD_OK;
 }
 
+int wgd_sample(wgd_context *ctx, const wgd_buffer *logits, uint32_t n, double temperature, uint32_t top_k,
+               double top_p, uint64_t seed, uint32_t index, int32_t *token) {
+  NEED_CTX(ctx); NEED_BUF(ctx, logits, "sample");
+  NEED_FIT(ctx, logits, (uint64_t)n * 4, "sample logits");
+  if (!token || !n || index > 0x7FFFFFFFu) return fail(ctx, WGD_E_INVALID, "wgd_sample: bad arguments");
+  if (!(temperature >= 0.0 && temperature <= 2.0) || top_k < 1 || top_k > 200 || !(top_p > 0.0 && top_p <= 1.0))
+    return fail(ctx, WGD_E_INVALID, "Invalid sampling settings.");
+  if (!ctx->sample_params) {
+    int rc = ctx_alloc(ctx, sizeof(SampleParams), "sampling settings", (void **)&ctx->sample_params);
+    if (rc) return rc;
+  }
+  const SampleParams p = {temperature, top_p, top_k, 0, seed};
+  int rc = ctx_check(ctx, hipMemcpyAsync(ctx->sample_params, &p, sizeof p, hipMemcpyHostToDevice, ctx->stream), "sample");
+  if (!rc) rc = ctx_check(ctx, sample(ctx->stream, (const float *)logits->ptr, n, ctx->sample_params, (int32_t)index,
+                                      nullptr, ctx->argmax_scratch, nullptr, 0, false), "sample");
+  if (!rc) rc = ctx_sync(ctx, "sample");
+  if (rc) return rc;
+  int32_t id = -1;
+  hipError_t e = hipMemcpy(&id, ctx->argmax_scratch, 4, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sample read-back");
+  *token = id;
+  if (id < 0) return fail(ctx, WGD_E_NONFINITE, "Inference produced non-finite logits. Stop and report this model/runtime combination.");
+  return WGD_OK;
+}
+
 int wgd_embed(wgd_context *ctx, int32_t type, const wgd_buffer *table, const wgd_buffer *ids, wgd_buffer *out,
               uint32_t hidden, uint32_t n, double scale) {
   NEED_CTX(ctx); NEED_BUF(ctx, table, "embed"); NEED_BUF(ctx, ids, "embed"); NEED_BUF(ctx, out, "embed");

@@ -118,11 +118,14 @@ class LoadOptions:
 
 @dataclass
 class GenerationOptions:
-    """engine.ts:21, validated as engine.ts:261-264."""
+    """engine.ts:21, validated as engine.ts:261-264, with the reference's defaults.
+    ``seed`` picks the uniforms that stand in for Math.random() (None: a fresh one per
+    call); the same seed, settings and prompt give the same tokens."""
     maxTokens: int = 128
-    temperature: float = 0.0
+    temperature: float = 0.7
     topK: int = 40
     topP: float = 0.9
+    seed: Optional[int] = None
 
 
 @dataclass
@@ -263,8 +266,14 @@ class PagedEngine:
                                                out.ctypes.data if logits else None, None))
         return out
 
+    def set_sampling(self, temperature: float, top_k: int = 40, top_p: float = 0.9, seed: int = 0) -> None:
+        """The token pick of forward_argmax and decode: greedy at temperature 0, else
+        sampled on the device with the uniforms of ``seed``."""
+        self.gpu.check(lib().wgd_model_sampling(self.model, float(temperature), int(top_k), float(top_p),
+                                                int(seed) & (2 ** 64 - 1)))
+
     def forward_argmax(self, ids: Sequence[int], start: int) -> int:
-        """forward + sample(T=0) with the argmax taken on the device."""
+        """forward + the token pick (greedy, or sampled: set_sampling) on the device."""
         n = len(ids)
         arr = (C.c_int32 * n)(*ids)
         tok = C.c_int32(-1)
@@ -280,7 +289,8 @@ class PagedEngine:
     # ------------------------------------------------------------------ generate
     def generate(self, prompt, options: Optional[GenerationOptions] = None, tokenizer=None,
                  chunk: int = 32, signal: Optional[AbortSignal] = None) -> Iterator[TokenEvent]:
-        """PagedEngine.generate (engine.ts:257-301) with greedy sampling.
+        """PagedEngine.generate (engine.ts:257-301): greedy at temperature 0, else top-k /
+        top-p sampling on the device (wgd_model_sampling).
 
         Prefix reuse, output limit, chunked prefill and the busy guard follow the
         reference; the decode loop runs on the device ``chunk`` tokens at a time.
@@ -300,8 +310,6 @@ class PagedEngine:
         if (not isinstance(t, (int, float)) or not math.isfinite(t) or t < 0 or t > 2 or not isinstance(k, int)
                 or k < 1 or k > 200 or not isinstance(p, (int, float)) or not math.isfinite(p) or p <= 0 or p > 1):
             raise ValueError("Invalid sampling settings.")
-        if t != 0:
-            raise ValueError("Only greedy decoding (temperature 0) is implemented by this runtime.")
         tokenizer = tokenizer if tokenizer is not None else self.tokenizer
         messages = isinstance(prompt, (list, tuple)) and len(prompt) > 0 and all(isinstance(m, dict) for m in prompt)
         if messages:
@@ -330,6 +338,8 @@ class PagedEngine:
         self.busy = True
         try:
             limit = output_limit(o.maxTokens, len(prompt), self.context)
+            seed = o.seed if o.seed is not None else int.from_bytes(os.urandom(8), "little")
+            self.set_sampling(o.temperature, o.topK, o.topP, seed)
             shared = 0
             while shared < len(prompt) and shared < len(self.tokensInCache) and prompt[shared] == self.tokensInCache[shared]:
                 shared += 1
@@ -391,11 +401,16 @@ class PagedEngine:
             self.gpu.dispose()
         self.tokensInCache = []
 
-    def sample(self, logits: np.ndarray) -> int:
-        """sample(T=0) (engine.ts:305-309) on the device: first strict maximum over finite
-        logits; raises when none is finite."""
+    def sample(self, logits: np.ndarray, temperature: float = 0.0, top_k: int = 40, top_p: float = 0.9,
+               seed: int = 0, index: int = 0) -> int:
+        """sample() (engine.ts:305-324) on the device: the first strict maximum over finite
+        logits at temperature 0, else a top-k / top-p draw with the index-th uniform of
+        ``seed``; raises when no logit is finite."""
         buf = self.gpu.upload(np.asarray(logits, np.float32), "sample logits")
         try:
-            return self.gpu.argmax(buf, int(np.asarray(logits).size))
+            n = int(np.asarray(logits).size)
+            if temperature == 0:
+                return self.gpu.argmax(buf, n)
+            return self.gpu.sample(buf, n, temperature, top_k, top_p, seed, index)
         finally:
             self.gpu.destroy(buf)

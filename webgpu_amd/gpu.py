@@ -54,6 +54,8 @@ SIGNATURES = {
     "wgd_bias_add": (C.c_int, [_P, _P, _P, _U32, _U32]),
     "wgd_activate": (C.c_int, [_P, _P, _U32]),
     "wgd_argmax": (C.c_int, [_P, _P, _U32, _P, C.POINTER(_I32)]),
+    "wgd_sample": (C.c_int, [_P, _P, _U32, C.c_double, _U32, C.c_double, C.c_uint64, _U32, C.POINTER(_I32)]),
+    "wgd_model_sampling": (C.c_int, [_P, C.c_double, _U32, C.c_double, C.c_uint64]),
     "wgd_embed": (C.c_int, [_P, _I32, _P, _P, _P, _U32, _U32, _D]),
     "wgd_model_create": (C.c_int, [_P, _P, C.POINTER(_I32), C.POINTER(_P)]),
     "wgd_model_tensor": (C.c_int, [_P, C.c_char_p, _I32, _I32, C.POINTER(_U64), _P, _U64]),
@@ -258,6 +260,14 @@ class Compute:
         idx = C.c_int32(-1)
         self.check(lib().wgd_argmax(self.ctx, logits.ptr, n, None, C.byref(idx)))
         return idx.value
+
+    def sample(self, logits: Buffer, n: int, temperature: float, top_k: int, top_p: float, seed: int,
+               index: int) -> int:
+        """sample() on the device with the index-th uniform of ``seed``."""
+        tok = C.c_int32(-1)
+        self.check(lib().wgd_sample(self.ctx, logits.ptr, n, float(temperature), int(top_k), float(top_p),
+                                    int(seed) & (2 ** 64 - 1), int(index), C.byref(tok)))
+        return tok.value
 
     def embed(self, type_: int, table: Buffer, ids: Buffer, out: Buffer, hidden: int, n: int, scale: float = 1.0) -> None:
         self.check(lib().wgd_embed(self.ctx, type_, table.ptr, ids.ptr, out.ptr, hidden, n, scale))
