@@ -58,6 +58,30 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
+// SMP_E logits per thread per step: SMP_E / 4 16-byte loads issued before any is used (one
+// workgroup's passes are bound by the round trip of each step: 256 KB per step keeps a
+// 128K-entry row to two), element e of the step at index base + 4 * (j * SMP_T + tid) + c
+// for e = 4 j + c. Entries past n read as NaN (not finite).
+constexpr int SMP_E = 64;
+constexpr uint32_t SMP_STEP = SMP_E * SMP_T;
+__device__ __forceinline__ void load_step(const float *logits, uint32_t n, uint32_t base, uint32_t tid,
+                                          float (&v)[SMP_E]) {
+#pragma unroll
+  for (int j = 0; j < SMP_E / 4; j++) {
+    const uint32_t i = base + 4 * (j * SMP_T + tid);
+    if (i + 3 < n) {
+      const float4 q = *(const float4 *)(logits + i);
+      v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++) v[4 * j + c] = i + c < n ? logits[i + c] : __uint_as_float(0x7FC00000u);
+    }
+  }
+}
+__device__ __forceinline__ uint32_t at_step(uint32_t base, uint32_t tid, int e) {
+  return base + 4 * ((e >> 2) * SMP_T + tid) + (e & 3);
+}
+
 struct SampleLds {
   uint32_t hist[SMP_BINS];
   uint64_t cand[SMP_CAND];
@@ -79,13 +103,17 @@ __global__ __launch_bounds__(SMP_T) void k_sample(const float *logits, uint32_t 
   __syncthreads();
   uint32_t cnt = 0;
   uint64_t best = 0;
-  for (uint32_t i = tid; i < n; i += SMP_T) {
-    const float v = logits[i];
-    if (!finite_f(v)) continue;
-    const uint64_t c = composite(v, i);
-    best = c > best ? c : best;
-    cnt++;
-    atomicAdd(&L.hist[c >> 52], 1u);
+  for (uint32_t base = 0; base < n; base += SMP_STEP) {
+    float v[SMP_E];
+    load_step(logits, n, base, tid, v);
+#pragma unroll
+    for (int e = 0; e < SMP_E; e++) {
+      if (!finite_f(v[e])) continue;
+      const uint64_t c = composite(v[e], at_step(base, tid, e));
+      best = c > best ? c : best;
+      cnt++;
+      atomicAdd(&L.hist[c >> 52], 1u);
+    }
   }
   cnt = wave_sum_u32(cnt);
   best = wave_max_u64(best);
@@ -140,11 +168,15 @@ __global__ __launch_bounds__(SMP_T) void k_sample(const float *logits, uint32_t 
       const uint32_t fmask = shift >= 12 ? 0xFFFu : (1u << shift) - 1;  // the next field's width
       for (uint32_t b = tid; b < SMP_BINS; b += SMP_T) L.hist[b] = 0;
       __syncthreads();
-      for (uint32_t i = tid; i < n; i += SMP_T) {
-        const float v = logits[i];
-        if (!finite_f(v)) continue;
-        const uint64_t c = composite(v, i);
-        if ((c & hi_mask) == prefix) atomicAdd(&L.hist[(uint32_t)((c >> nshift) & fmask)], 1u);
+      for (uint32_t base = 0; base < n; base += SMP_STEP) {
+        float v[SMP_E];
+        load_step(logits, n, base, tid, v);
+#pragma unroll
+        for (int e = 0; e < SMP_E; e++) {
+          if (!finite_f(v[e])) continue;
+          const uint64_t c = composite(v[e], at_step(base, tid, e));
+          if ((c & hi_mask) == prefix) atomicAdd(&L.hist[(uint32_t)((c >> nshift) & fmask)], 1u);
+        }
       }
       __syncthreads();
       shift = nshift;
@@ -154,24 +186,22 @@ __global__ __launch_bounds__(SMP_T) void k_sample(const float *logits, uint32_t 
     if (tid == 0) L.ncand = 0;
     for (uint32_t j = tid; j < SMP_CAND; j += SMP_T) L.cand[j] = 0;
     __syncthreads();
-    for (uint32_t i0 = 0; i0 < n; i0 += SMP_T) {
-      const uint32_t i = i0 + tid;
-      bool take = false;
-      uint64_t c = 0;
-      if (i < n) {
-        const float v = logits[i];
-        if (finite_f(v)) {
-          c = composite(v, i);
-          take = c >= lo;
+    for (uint32_t base = 0; base < n; base += SMP_STEP) {
+      float v[SMP_E];
+      load_step(logits, n, base, tid, v);
+#pragma unroll
+      for (int e = 0; e < SMP_E; e++) {
+        const bool fin = finite_f(v[e]);
+        const uint64_t c = fin ? composite(v[e], at_step(base, tid, e)) : 0;
+        const bool take = fin && c >= lo;
+        const uint64_t m = __ballot(take);
+        if (m) {
+          uint32_t slot0 = 0;
+          if (lane == 0) slot0 = atomicAdd(&L.ncand, (uint32_t)__popcll(m));
+          slot0 = __shfl(slot0, 0);
+          const uint32_t slot = slot0 + (uint32_t)__popcll(m & ((1ull << lane) - 1));
+          if (take && slot < SMP_CAND) L.cand[slot] = c;
         }
-      }
-      const uint64_t m = __ballot(take);
-      if (m) {
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(&L.ncand, (uint32_t)__popcll(m));
-        base = __shfl(base, 0);
-        const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1));
-        if (take && slot < SMP_CAND) L.cand[slot] = c;
       }
     }
     __syncthreads();
