@@ -11,6 +11,7 @@ function scripted(context, batch, caps) {
   eng.forwardArgmax = () => 7;
   eng.decode = (token, start, count) => { eng.counts.push(count); return new Array(count).fill(7); };
   eng.stats = () => ({});
+  eng.setSampling = () => {};
   return eng;
 }
 

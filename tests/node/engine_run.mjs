@@ -1,11 +1,12 @@
 // Drives the Node host end to end and prints JSON for the pytest wrapper: argv is
-// <gguf path> <mode> [prompt ids comma-separated] [max tokens].
+// <gguf path> <mode> [prompt ids comma-separated] [max tokens] [temperature:seed].
 //   config: modelConfig + attentionMemory of the file (no GPU)
 //   greedy: load, last-row logits of forward(ids, 0), then generate(ids, maxTokens) ids
+//           (sampled with the given temperature and seed when the last argument is set)
 import { readGGUF, modelConfig, FileSource } from '../../webgpu_amd/node/gguf.mjs';
 import { attentionMemory } from '../../webgpu_amd/node/context.mjs';
 
-const [path, mode, idsArg, maxArg] = process.argv.slice(2);
+const [path, mode, idsArg, maxArg, sampleArg] = process.argv.slice(2);
 
 async function main() {
   if (mode === 'config') {
@@ -25,7 +26,8 @@ async function main() {
     const logits = eng.forward(ids, 0, true);
     eng.reset();
     const tokens = [];
-    for await (const ev of eng.generate(ids, { maxTokens: Number(maxArg) })) tokens.push(ev.token);
+    const [temperature, seed] = sampleArg ? sampleArg.split(':').map(Number) : [0, 0];
+    for await (const ev of eng.generate(ids, { maxTokens: Number(maxArg), temperature, seed })) tokens.push(ev.token);
     console.log(JSON.stringify({ adapter: info.adapter, logits: Array.from(logits), tokens, gpuBytes: info.stats.gpuBytes }));
   } finally {
     eng.dispose();

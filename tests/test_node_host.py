@@ -58,7 +58,8 @@ def test_addon_exports_engine_surface():
     r = subprocess.run([NODE, "-e", code], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     assert json.loads(r.stdout) == sorted(["create", "destroy", "adapterName", "memory", "done", "modelCreate",
-                                           "modelTensor", "modelReady", "modelForward", "modelDecode", "modelDestroy"])
+                                           "modelTensor", "modelReady", "modelForward", "modelDecode", "modelSampling",
+                                           "modelDestroy"])
 
 
 @needs_node
@@ -105,3 +106,21 @@ def test_node_engine_tiny_greedy_matches_oracle(tiny_file):
     err = float(np.abs(logits - want).max() / np.abs(want).max())
     assert err <= 1e-3, err
     assert got["tokens"] == list(expected)
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_and_python_hosts_sample_the_same_tokens(tiny_file):
+    # both hosts set the same device token pick: one seed, one sequence
+    from webgpu_amd.engine import GenerationOptions, LoadOptions, PagedEngine
+    path, f = tiny_file
+    c = model_config(parse_gguf_header(f, f.size))
+    ids = synth.prompt_ids(c.vocab, 8)
+    got = run_node(path, "greedy", ",".join(map(str, ids)), 24, "1.1:987654321", timeout=300)
+    eng = PagedEngine()
+    eng.load(path, LoadOptions(contextLength=512, batchSize=128))
+    try:
+        want = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=24, temperature=1.1, seed=987654321))]
+    finally:
+        eng.dispose()
+    assert got["tokens"] == want and len(want) == 24

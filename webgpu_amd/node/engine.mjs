@@ -1,8 +1,8 @@
 // engine.mjs — PagedEngine for the Node host (src/core/engine.ts:26-324) over the libwgd
 // N-API addon: load(path, options) -> ModelInfo, async generate(prompt ids, options) ->
-// TokenEvents, forward, reset, dispose, info and the greedy sample. GGUF parsing,
+// TokenEvents, forward, reset, dispose, info and the device token pick. GGUF parsing,
 // modelConfig and ring sizing run here as in gguf.ts / context.ts; weights are uploaded
-// once and stay resident (the weight pager collapses), and every forward and greedy decode
+// once and stay resident (the weight pager collapses), and every forward and decode
 // step runs in libwgd on the GPU. Tokenizers are outside this runtime: prompts are ids, or
 // any object with chat(messages) -> ids, decode(ids) -> string and eos passed as tokenizer.
 import { createRequire } from 'module';
@@ -113,12 +113,19 @@ export class PagedEngine {
     return addon.modelForward(this.model, Int32Array.from(ids), start, null);
   }
 
-  /** `count` greedy steps on the device from `token` at position `start`. */
+  /** The token pick of forwardArgmax and decode: greedy at temperature 0, else top-k /
+   * top-p sampling on the device with the uniforms of `seed` (an integer below 2^53). */
+  setSampling(temperature, topK = 40, topP = 0.9, seed = 0) {
+    addon.modelSampling(this.model, temperature, topK, topP, Math.floor(seed / 4294967296) >>> 0, seed >>> 0);
+  }
+
+  /** `count` decode steps on the device from `token` at position `start`. */
   decode(token, start, count) {
     return Array.from(addon.modelDecode(this.model, token, start, count));
   }
 
-  /** PagedEngine.generate (engine.ts:257-301), greedy: prefix reuse, output limit, chunked
+  /** PagedEngine.generate (engine.ts:257-301), greedy or sampled on the device (the
+   * reference's GenerationOptions defaults, plus `seed`): prefix reuse, output limit, chunked
    * prefill and the busy guard; the decode loop runs on the device `chunk` tokens at a time.
    * A chunk may run past an end-of-turn token; a sliding ring keeps the window plus one
    * prompt batch, so on models with one the chunk is capped to the batch. An aborted
@@ -126,11 +133,10 @@ export class PagedEngine {
   async *generate(prompt, options = {}, tokenizer = null, chunk = 32, signal = undefined) {
     if (this.busy) throw new Error('A generation is already running.');
     if (this.disposed || !this.model) throw new Error('Load a model first.');
-    const o = Object.assign({ maxTokens: 128, temperature: 0, topK: 40, topP: 0.9 }, options);
+    const o = Object.assign({ maxTokens: 128, temperature: 0.7, topK: 40, topP: 0.9, seed: null }, options);
     if (!Number.isInteger(o.maxTokens) || o.maxTokens < 1 || o.maxTokens > MAX_CONTEXT) throw new Error(`maxTokens must be 1–${MAX_CONTEXT}.`);
     if (!Number.isFinite(o.temperature) || o.temperature < 0 || o.temperature > 2 || !Number.isInteger(o.topK) || o.topK < 1 ||
         o.topK > 200 || !Number.isFinite(o.topP) || o.topP <= 0 || o.topP > 1) throw new Error('Invalid sampling settings.');
-    if (o.temperature !== 0) throw new Error('Only greedy decoding (temperature 0) is implemented by this runtime.');
     const ids = tokenizer ? Array.from(tokenizer.chat(prompt)) : Array.from(prompt, Number);
     if (!ids.length) throw new Error('Provide a non-empty prompt.');
     const eos = new Set((tokenizer && tokenizer.eos) || []);
@@ -138,6 +144,7 @@ export class PagedEngine {
     this.busy = true;
     try {
       const limit = outputLimit(o.maxTokens, ids.length, this.context);
+      this.setSampling(o.temperature, o.topK, o.topP, o.seed === null ? Math.floor(Math.random() * 2 ** 53) : o.seed);
       let shared = 0;
       while (shared < ids.length && shared < this.tokensInCache.length && ids[shared] === this.tokensInCache[shared]) shared++;
       shared = Math.min(shared, ids.length - 1);

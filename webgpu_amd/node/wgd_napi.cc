@@ -273,6 +273,22 @@ napi_value model_decode(napi_env env, napi_callback_info info) {
   return arr;
 }
 
+// modelSampling(model, temperature, topK, topP, seedHi, seedLo): the token pick of
+// modelForward / modelDecode (temperature 0: greedy); the seed as two 32-bit halves
+napi_value model_sampling(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  Model *w = live_model(env, argv[0]);
+  if (!w) return nullptr;
+  double t = 0, p = 0, hi = 0, lo = 0;
+  int32_t k = 0;
+  if (!get_f64(env, argv[1], &t) || !get_i32(env, argv[2], &k) || !get_f64(env, argv[3], &p) ||
+      !get_f64(env, argv[4], &hi) || !get_f64(env, argv[5], &lo) || k < 0)
+    return throw_msg(env, "WGD_E_INVALID", "Invalid sampling settings.");
+  const uint64_t seed = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+  CHECK(w->owner->ctx, wgd_model_sampling(w->m, t, (uint32_t)k, p, seed));
+  return undefined(env);
+}
+
 napi_value model_destroy(napi_env env, napi_callback_info info) {
   ARGS(1);
   Model *w = unwrap<Model>(env, argv[0]);
@@ -286,7 +302,7 @@ napi_value init(napi_env env, napi_value exports) {
       {"create", create}, {"destroy", destroy}, {"adapterName", adapter_name}, {"memory", memory},
       {"done", done}, {"modelCreate", model_create}, {"modelTensor", model_tensor},
       {"modelReady", model_ready}, {"modelForward", model_forward}, {"modelDecode", model_decode},
-      {"modelDestroy", model_destroy}};
+      {"modelSampling", model_sampling}, {"modelDestroy", model_destroy}};
   for (auto &f : fns) {
     napi_value fn;
     napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);
