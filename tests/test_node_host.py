@@ -124,3 +124,41 @@ def test_node_and_python_hosts_sample_the_same_tokens(tiny_file):
     finally:
         eng.dispose()
     assert got["tokens"] == want and len(want) == 24
+
+
+@needs_node
+def test_node_runtime_api_rules_without_a_device():
+    # sdk.mjs + worker.mjs with a scripted engine in the worker thread
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "sdk_rules.mjs")], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 0, r.stderr[-3000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["noModel"] == ["Error", "Load a model first."]
+    assert out["badLoad"] == ["Error", "Unsupported GGUF version."]
+    assert out["info"]["fileBytes"] == 123 and out["progress"] == [0.5]
+    assert out["tokens"] == [0, 1, 2, 3, 4] and out["first"] == 0
+    assert out["busy"] == ["Error", "The runtime is busy."]
+    assert out["stopped"] == ["AbortError", "Stopped by user"]
+    assert out["afterStop"] == 3 and out["afterBreak"] == 4
+    assert out["pending"] == ["Error", "Runtime disposed."]
+    assert out["disposed"] == ["Error", "This runtime was disposed. Create a new WebGPU instance."]
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_runtime_api_drives_the_engine(tiny_file):
+    from webgpu_amd.engine import GenerationOptions, LoadOptions, PagedEngine
+    path, f = tiny_file
+    c = model_config(parse_gguf_header(f, f.size))
+    ids = synth.prompt_ids(c.vocab, 8)
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "sdk_run.mjs"), path, ",".join(map(str, ids)), "6"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    got = json.loads(r.stdout.strip().splitlines()[-1])
+    eng = PagedEngine()
+    eng.load(path, LoadOptions(contextLength=512, batchSize=128))
+    try:
+        want = [e.token for e in eng.generate(ids, GenerationOptions(maxTokens=6, temperature=0))]
+    finally:
+        eng.dispose()
+    assert got == {"batchSize": 128, "tokens": want}
