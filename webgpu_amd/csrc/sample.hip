@@ -101,20 +101,22 @@ __global__ __launch_bounds__(SMP_T) void k_sample(const float *logits, uint32_t 
   // pass A: finite count, best composite, histogram of bits 63..52
   for (uint32_t b = tid; b < SMP_BINS; b += SMP_T) L.hist[b] = 0;
   __syncthreads();
-  uint32_t cnt = 0;
-  uint64_t best = 0;
+  // 32-bit keys here (the passes are VALU-bound in one workgroup): a thread visits its
+  // indices in increasing order, so a strict > keeps its first maximum
+  uint32_t cnt = 0, bkey = 0, bidx = 0;
   for (uint32_t base = 0; base < n; base += SMP_STEP) {
     float v[SMP_E];
     load_step(logits, n, base, tid, v);
 #pragma unroll
     for (int e = 0; e < SMP_E; e++) {
       if (!finite_f(v[e])) continue;
-      const uint64_t c = composite(v[e], at_step(base, tid, e));
-      best = c > best ? c : best;
+      const uint32_t k = order_key(v[e]);
+      if (k > bkey) { bkey = k; bidx = at_step(base, tid, e); }
       cnt++;
-      atomicAdd(&L.hist[c >> 52], 1u);
+      atomicAdd(&L.hist[k >> 20], 1u);
     }
   }
+  uint64_t best = bkey ? ((uint64_t)bkey << 32) | (0xFFFFFFFFu - bidx) : 0;
   cnt = wave_sum_u32(cnt);
   best = wave_max_u64(best);
   if (lane == 0) { L.wsum[wv] = cnt; L.wmax[wv] = best; }
@@ -186,14 +188,19 @@ __global__ __launch_bounds__(SMP_T) void k_sample(const float *logits, uint32_t 
     if (tid == 0) L.ncand = 0;
     for (uint32_t j = tid; j < SMP_CAND; j += SMP_T) L.cand[j] = 0;
     __syncthreads();
+    // without refinement the bound has no index bits: compare the 32-bit keys
+    const bool keys_only = (lo & 0xFFFFFFFFull) == 0;
+    const uint32_t lo_key = (uint32_t)(lo >> 32);
     for (uint32_t base = 0; base < n; base += SMP_STEP) {
       float v[SMP_E];
       load_step(logits, n, base, tid, v);
 #pragma unroll
       for (int e = 0; e < SMP_E; e++) {
         const bool fin = finite_f(v[e]);
-        const uint64_t c = fin ? composite(v[e], at_step(base, tid, e)) : 0;
-        const bool take = fin && c >= lo;
+        const uint32_t k = fin ? order_key(v[e]) : 0;
+        const bool pre = fin && k >= lo_key;  // a superset of the composites >= lo
+        const uint64_t c = pre ? ((uint64_t)k << 32) | (0xFFFFFFFFu - at_step(base, tid, e)) : 0;
+        const bool take = pre && (keys_only || c >= lo);
         const uint64_t m = __ballot(take);
         if (m) {
           uint32_t slot0 = 0;
