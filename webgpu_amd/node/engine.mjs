@@ -3,7 +3,7 @@
 // TokenEvents, forward, reset, dispose, info and the device token pick. GGUF parsing,
 // modelConfig and ring sizing run here as in gguf.ts / context.ts; weights are uploaded
 // once and stay resident (the weight pager collapses), and every forward and decode
-// step runs in libwgd on the GPU. Tokenizers are outside this runtime: prompts are ids, or
+// step runs in libwgd on the GPU. The host keeps the reference's tokenizers: prompts are ids, or
 // any object with chat(messages) -> ids, decode(ids) -> string and eos passed as tokenizer.
 import { createRequire } from 'module';
 import { readGGUF, modelConfig, FileSource } from './gguf.mjs';
@@ -107,7 +107,7 @@ export class PagedEngine {
     return out;
   }
 
-  /** forward + sample(T=0) with the argmax taken on the device. */
+  /** forward + the token pick on the device (greedy, or sampled: setSampling). */
   forwardArgmax(ids, start) {
     if (!this.model) throw new Error('Load a model first.');
     return addon.modelForward(this.model, Int32Array.from(ids), start, null);
