@@ -19,7 +19,7 @@
 // (4096 bins, LDS atomics); a block scan finds the bin holding the k-th largest. If the
 // bins above it and it hold at most 1024 composites, pass B gathers them into LDS;
 // otherwise the next 12 bits of that bin are histogrammed the same way (values that tie
-// over many indices), until they fit. A bitonic sort orders the gathered composites.
+// over many indices), until they fit. Each gathered composite's rank among them orders them.
 #include "internal.h"
 #include "decode.h"
 
@@ -212,17 +212,18 @@ __global__ __launch_bounds__(SMP_T) void k_sample(const float *logits, uint32_t 
       }
     }
     __syncthreads();
-    // bitonic sort, descending
-    for (uint32_t k = 2; k <= SMP_CAND; k <<= 1)
-      for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-        const uint32_t i = tid, l = i ^ j;
-        if (l > i) {
-          const uint64_t a = L.cand[i], b = L.cand[l];
-          const bool desc = (i & k) == 0;
-          if (desc ? a < b : a > b) { L.cand[i] = b; L.cand[l] = a; }
-        }
-        __syncthreads();
-      }
+    // rank sort, descending: the composites are unique, so each one's place is the count of
+    // larger ones (one barrier instead of a sorting network's)
+    const uint32_t nc = L.ncand < SMP_CAND ? L.ncand : SMP_CAND;
+    uint64_t mine = 0;
+    uint32_t rank = 0;
+    if (tid < nc) {
+      mine = L.cand[tid];
+      for (uint32_t j = 0; j < nc; j++) rank += L.cand[j] > mine ? 1u : 0u;
+    }
+    __syncthreads();
+    if (tid < nc) L.cand[rank] = mine;
+    __syncthreads();
     // probabilities of the top K (f64, as the reference's numbers)
     const double bestv = (double)logits[comp_index(best)];
     if (tid < K) L.prob[tid] = exp(((double)logits[comp_index(L.cand[tid])] - bestv) / p.temperature);
