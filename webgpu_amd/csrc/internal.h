@@ -114,9 +114,11 @@ struct StepState { int32_t pos, token, step, error; };
 struct SampleParams { double temperature, top_p; uint32_t top_k, pad; uint64_t seed; };
 // sample() of engine.ts:305-324 on logits[0..n): the token to *out, drawn with the index-th
 // uniform of the seed (index < 0: st->pos + 1); with `advance`, recorded in st and
-// tokens[st->step] and the position advanced, as the greedy step does.
+// tokens[st->step] and the position advanced, as the greedy step does. `scratch` holds
+// sample_scratch_bytes(n) of device memory (the slices' candidates).
+uint64_t sample_scratch_bytes(uint32_t n);
 hipError_t sample(hipStream_t s, const float *logits, uint32_t n, const SampleParams *params, int32_t index,
-                  StepState *st, int32_t *out, int32_t *tokens, uint32_t cap, bool advance);
+                  StepState *st, int32_t *out, int32_t *tokens, uint32_t cap, bool advance, void *scratch);
 uint64_t gemm_group_split_floats(const GemmGroup &g, uint32_t batch);
 hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_t batch, GemmScratch *scratch);
 // y[b*stride + row_base + r] = sum_c deq(W)[r][c] * x[(b+input_offset)*cols + c]: the

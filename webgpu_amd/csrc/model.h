@@ -28,6 +28,8 @@ struct wgd_context {
   uint16_t *gemm_xs = nullptr;        // its input split into bf16 (hi, lo)
   uint64_t gemm_xs_elems = 0;
   wgd::SampleParams *sample_params = nullptr;  // settings of wgd_sample
+  void *sample_scratch = nullptr;              // its slices' candidates
+  uint64_t sample_scratch_bytes = 0;
 };
 
 namespace wgd {

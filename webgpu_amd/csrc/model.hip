@@ -81,6 +81,7 @@ struct wgd_model {
   // the sampling variant of the decode step (its own graph); settings in device memory
   bool sampling = false;
   SampleParams *sample_params = nullptr;
+  void *sample_scratch = nullptr;
   hipGraph_t graph_s = nullptr;
   hipGraphExec_t exec_s = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -473,7 +474,7 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
   WGD_HIP(mv(s, W, nullptr, qv(m->qx_head, H, true, c.epsilon), m->logits, MV_STORE, &hout));
   if (m->sampling)
     return sample(s, m->logits, c.vocab, m->sample_params, -1, m->state, m->argmax_buf, m->tokens,
-                  (uint32_t)c.context, advance);
+                  (uint32_t)c.context, advance, m->sample_scratch);
   hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(256), 0, s, (const uint64_t *)m->arg_part, m->arg_entries,
                      m->argmax_buf, m->state, m->tokens, (uint32_t)m->c.context, advance ? 1 : 0);
   return hipGetLastError();
@@ -488,7 +489,7 @@ hipError_t decode_step_generic(wgd_model *m, bool advance) {
   WGD_HIP(head(m, 0));
   if (m->sampling)
     return sample(s, m->logits, m->c.vocab, m->sample_params, -1, m->state, m->argmax_buf, m->tokens,
-                  (uint32_t)m->c.context, advance);
+                  (uint32_t)m->c.context, advance, m->sample_scratch);
   if (advance) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, m->state, (const int32_t *)m->argmax_buf, m->tokens,
                        (uint32_t)m->c.context);
@@ -568,6 +569,7 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
   rc = rc ? rc : alloc_t(m, (uint64_t)c.context + 1, "decode tokens", &m->tokens);
   rc = rc ? rc : alloc_t(m, 2 + 2 * 256, "argmax", &m->argmax_buf);
   rc = rc ? rc : alloc_t(m, 1, "sampling settings", &m->sample_params);
+  rc = rc ? rc : alloc(m, sample_scratch_bytes((uint32_t)c.vocab), "sampling candidates", &m->sample_scratch);
   m->att_part_floats = attention_scratch_floats(c.heads, c.head_dim, 1, (uint32_t)device_cu_count() * 4);
   if (decode_attention_supported(c.heads, c.kv_heads, c.head_dim))
     for (int l = 0; l < c.layers; l++)
@@ -823,7 +825,7 @@ int wgd_model_forward(wgd_model *m, const int32_t *ids, int32_t n, int32_t start
     // the next token takes position start + n
     if (!rc && want && m->sampling)
       rc = ctx_check(ctx, sample(s, m->logits, m->c.vocab, m->sample_params, start + n, nullptr, m->argmax_buf, nullptr, 0,
-                                 false), "sample");
+                                 false, m->sample_scratch), "sample");
   }
   if (!rc) rc = ctx_sync(ctx, "GPU fault during forward");
   if (rc) return rc;

@@ -477,8 +477,15 @@ int wgd_sample(wgd_context *ctx, const wgd_buffer *logits, uint32_t n, double te
   }
   const SampleParams p = {temperature, top_p, top_k, 0, seed};
   int rc = ctx_check(ctx, hipMemcpyAsync(ctx->sample_params, &p, sizeof p, hipMemcpyHostToDevice, ctx->stream), "sample");
+  if (!rc && ctx->sample_scratch_bytes < sample_scratch_bytes(n)) {
+    if (ctx->sample_scratch) ctx_free(ctx, ctx->sample_scratch);
+    ctx->sample_scratch = nullptr;
+    ctx->sample_scratch_bytes = 0;
+    rc = ctx_alloc(ctx, sample_scratch_bytes(n), "sampling candidates", &ctx->sample_scratch);
+    if (!rc) ctx->sample_scratch_bytes = sample_scratch_bytes(n);
+  }
   if (!rc) rc = ctx_check(ctx, sample(ctx->stream, (const float *)logits->ptr, n, ctx->sample_params, (int32_t)index,
-                                      nullptr, ctx->argmax_scratch, nullptr, 0, false), "sample");
+                                      nullptr, ctx->argmax_scratch, nullptr, 0, false, ctx->sample_scratch), "sample");
   if (!rc) rc = ctx_sync(ctx, "sample");
   if (rc) return rc;
   int32_t id = -1;
