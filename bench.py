@@ -222,6 +222,9 @@ def main() -> None:
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the matvec microbench and a 256 MiB device copy (counter calibration), no JSON line")
     ap.add_argument("--gemm-only", action="store_true", help="only the prompt-GEMM microbench, no JSON line")
+    ap.add_argument("--sample-only", action="store_true",
+                    help="only the device sampler (T 0.7, top-k 40, top-p 0.9) on normal logits rows of three vocabulary "
+                         "sizes, 30 draws each, no JSON line")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the token loop runs on a single MI355X (multi-GPU sharding is a design "
@@ -245,6 +248,19 @@ def main() -> None:
             m = matvec_bench(gpu, ev, *s)
             print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
                   f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+        gpu.dispose()
+        return
+    if a.sample_only:
+        gpu = Compute().init()
+        rng = np.random.default_rng(0)
+        for n in (128256, 151936, 262144):
+            buf = gpu.upload((rng.standard_normal(n) * 3).astype(np.float32), "logits")
+            t0 = time.perf_counter()
+            for i in range(30):
+                gpu.sample(buf, n, 0.7, 40, 0.9, 1, i)
+            print(f"[bench] sample {n} entries: {(time.perf_counter() - t0) / 30 * 1e6:.1f} us per call "
+                  f"(host round trip included)", file=sys.stderr, flush=True)
+            gpu.destroy(buf)
         gpu.dispose()
         return
     if a.gemm_only:
