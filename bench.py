@@ -323,9 +323,22 @@ def main() -> None:
     value = a.steps / dt
     print(f"[bench] decode {a.steps} tokens in {dt * 1e3:.1f} ms -> {value:.1f} tok/s", file=sys.stderr, flush=True)
 
+    # the same decode with the reference's default sampling (reported, not the metric): the
+    # same positions again, each step drawing on the device (its own decode graph)
+    eng.set_sampling(0.7, 40, 0.9, seed=1)
+    eng.decode(token, pos, 2)
+    eng.gpu.done()
+    t0 = time.perf_counter()
+    eng.decode(token, pos, a.steps)
+    eng.gpu.done()
+    sampled = a.steps / (time.perf_counter() - t0)
+    eng.set_sampling(0.0)
+    print(f"[bench] decode with sampling (T 0.7, top-k 40, top-p 0.9): {sampled:.1f} tok/s", file=sys.stderr, flush=True)
+
     result = {
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": dt * 1e3 / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "decode_sampled_tok_s": sampled,
         "dtype": "f32", "data": "synthetic (seeded random-init Q4_K_M GGUF)",
         "config": {"workload": f"{a.model}-shape Q4_K_M greedy decode", "prompt": a.prompt, "prefill_batch": 128,
                    "decode_tokens": a.steps, "context": context, "kv_cache": "f32",
