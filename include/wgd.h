@@ -212,10 +212,11 @@ int wgd_model_ready(wgd_model *m);
  * is finite: the greedy id, or with sampling set the draw for position start + n). */
 int wgd_model_forward(wgd_model *m, const int32_t *ids, int32_t n, int32_t start,
                       float *logits, int32_t *argmax);
-/* The greedy decode loop of generate (engine.ts:290-298) kept on the device: for
- * i < count, run forward([token_i], start+i) and take token_{i+1} = argmax; token_0 =
- * `token`. Writes token_1..token_count to out_tokens. Each step is one replay of a
- * captured HIP graph; positions and ids never leave the device between steps. */
+/* The decode loop of generate (engine.ts:290-298) kept on the device: for i < count, run
+ * forward([token_i], start+i) and take token_{i+1} by the model's token pick (greedy, or
+ * sampled as set by wgd_model_sampling); token_0 = `token`. Writes token_1..token_count to
+ * out_tokens. Each step is one replay of a captured HIP graph (one per pick mode);
+ * positions and ids never leave the device between steps. */
 int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count,
                      int32_t *out_tokens);
 /* The token pick of generate (engine.ts:261-264, 292, 305-324) for wgd_model_forward and
