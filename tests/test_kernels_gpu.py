@@ -361,6 +361,14 @@ def test_bounds_checks_reject_overruns(gpu):
         gpu.matmul(Q4_K, w, x, y, 256, 2, 2, 0, 0, 1)  # 2 rows need 288 weight bytes
     with pytest.raises(WgdError):
         gpu.matmul(Q4_K, w, x, y, 256, 1, 1, 1, 0, 1)  # rowBase 1 writes past y
+    # offsets whose sum with the size wraps 64 bits are outside the buffers too
+    with pytest.raises(WgdError):
+        gpu.copy(x, y, 4, 2 ** 64 - 2, 0)
+    with pytest.raises(WgdError):
+        gpu.copy(x, y, 4, 0, 2 ** 64 - 2)
+    with pytest.raises(WgdError):
+        gpu.copy(x, y, 8, 0, 0)  # 8 bytes into the 4-byte y
+    gpu.copy(x, y, 4, 4, 0)
     for b in (w, x, y):
         gpu.destroy(b)
 

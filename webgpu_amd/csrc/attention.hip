@@ -323,25 +323,11 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnK a) {
 }
 
 template <uint32_t HD>
-static hipError_t launch_attn_prompt(hipStream_t s, AttnK a, const AttnArgs &in, uint32_t keys) {
+static hipError_t launch_attn_prompt(hipStream_t s, AttnK a, const AttnArgs &in, uint32_t nsplit) {
   const uint32_t nqt = (in.batch + 15) / 16;
-  const uint32_t wgs = in.kv_heads * ((nqt * a.group + 3) / 4);
-  const uint32_t tiles = (keys + AP_T - 1) / AP_T;
-  const uint32_t want = ((uint32_t)device_cu_count() + wgs - 1) / wgs;
-  uint32_t nsplit = tiles < want ? tiles : want;
-  if (nsplit < 1) nsplit = 1;
-  if (nsplit > 1) {
-    const uint64_t per_split = (uint64_t)in.batch * in.heads * (in.hd + 2);
-    const uint64_t fit = in.partial ? in.partial_floats / per_split : 0;
-    if (fit < nsplit) nsplit = fit > 1 ? (uint32_t)fit : 1;
-  }
   a.nsplit = nsplit;
   constexpr size_t lds = attn_prompt_lds<HD>();
-  static bool big_lds = false;
-  if (lds > 65536 && !big_lds) {
-    WGD_HIP(hipFuncSetAttribute((const void *)k_attn_prompt<HD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    big_lds = true;
-  }
+  if (lds > 65536) lds_opt_in((const void *)k_attn_prompt<HD>);
   hipLaunchKernelGGL(k_attn_prompt<HD>, dim3(in.kv_heads, (nqt * a.group + 3) / 4, nsplit), dim3(256), lds, s, a);
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
@@ -365,15 +351,12 @@ uint64_t attention_scratch_floats(uint32_t heads, uint32_t hd, uint32_t batch, u
   return (uint64_t)max_splits * batch * heads * (hd + 2);
 }
 
-hipError_t attention(hipStream_t s, const AttnArgs &in) {
-  if (!in.batch) return hipSuccess;
-  if (!in.kv_heads || in.heads % in.kv_heads || in.hd == 0 || in.hd > 512 || !in.capacity || !in.window)
-    return hipErrorInvalidValue;
-  AttnK a;
-  a.q = in.q; a.k = in.k; a.v = in.v; a.y = in.y; a.part = in.partial;
-  a.heads = in.heads; a.kvh = in.kv_heads; a.hd = in.hd; a.start = in.start; a.start_dev = in.start_dev;
-  a.scale = in.scale; a.window = in.window; a.capacity = in.capacity; a.batch = in.batch;
-  a.group = in.heads / in.kv_heads;
+// How a launch runs: the MFMA prompt kernel (hd 64/128/256 with 16-byte aligned operands) or
+// the generic one (query blocks of qb tokens, tiles of T keys), and the number of key
+// chunks: as many as fill the chip, fewer when `partial_floats` holds fewer partials.
+struct AttnPlan { uint32_t mfma_hd, nsplit, qb, R, T, qblocks; };
+static bool attn_plan(const AttnArgs &in, uint64_t partial_floats, AttnPlan &p) {
+  const uint32_t group = in.heads / in.kv_heads;
   // Key range bound: the host start when known, else the whole ring/window.
   uint32_t keys = in.window;
   if (!in.start_dev) {
@@ -385,32 +368,61 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
     keys = in.capacity + in.batch;
   }
   const bool aligned = ((uintptr_t)in.q | (uintptr_t)in.k | (uintptr_t)in.v | (uintptr_t)in.y) % 16 == 0;
-  if (aligned && in.hd == 64) return launch_attn_prompt<64>(s, a, in, keys);
-  if (aligned && in.hd == 128) return launch_attn_prompt<128>(s, a, in, keys);
-  if (aligned && in.hd == 256) return launch_attn_prompt<256>(s, a, in, keys);
-  a.qb = a.group >= 16 ? 1 : 16 / a.group;
-  if (a.qb > in.batch) a.qb = in.batch;
-  a.R = a.qb * a.group;
-  if (a.R > 16) return hipErrorInvalidValue;
-  a.T = tile_keys(in.hd);
-  const uint32_t qblocks = (in.batch + a.qb - 1) / a.qb;
-  uint32_t tiles = (keys + a.T - 1) / a.T;
-  uint32_t want = (uint32_t)device_cu_count() * 4 / (in.kv_heads * qblocks);
+  p = AttnPlan{};
+  uint32_t tiles, want;
+  if (aligned && (in.hd == 64 || in.hd == 128 || in.hd == 256)) {
+    p.mfma_hd = in.hd;
+    const uint32_t nqt = (in.batch + 15) / 16;
+    const uint32_t wgs = in.kv_heads * ((nqt * group + 3) / 4);
+    tiles = (keys + AP_T - 1) / AP_T;
+    want = ((uint32_t)device_cu_count() + wgs - 1) / wgs;
+  } else {
+    p.qb = group >= 16 ? 1 : 16 / group;
+    if (p.qb > in.batch) p.qb = in.batch;
+    p.R = p.qb * group;
+    if (p.R > 16) return false;
+    p.T = tile_keys(in.hd);
+    p.qblocks = (in.batch + p.qb - 1) / p.qb;
+    tiles = (keys + p.T - 1) / p.T;
+    want = (uint32_t)device_cu_count() * 4 / (in.kv_heads * p.qblocks);
+  }
   uint32_t nsplit = tiles < want ? tiles : want;
   if (nsplit < 1) nsplit = 1;
   if (nsplit > 1) {
-    uint64_t per_split = (uint64_t)in.batch * in.heads * (in.hd + 2);
-    uint64_t fit = in.partial ? in.partial_floats / per_split : 0;
+    const uint64_t per_split = (uint64_t)in.batch * in.heads * (in.hd + 2);
+    const uint64_t fit = partial_floats / per_split;
     if (fit < nsplit) nsplit = fit > 1 ? (uint32_t)fit : 1;
   }
+  p.nsplit = nsplit;
+  return true;
+}
+
+uint64_t attention_partial_need(const AttnArgs &in) {
+  AttnPlan p;
+  if (!in.batch || !in.kv_heads || in.heads % in.kv_heads || !attn_plan(in, UINT64_MAX, p) || p.nsplit < 2) return 0;
+  return (uint64_t)p.nsplit * in.batch * in.heads * (in.hd + 2);
+}
+
+hipError_t attention(hipStream_t s, const AttnArgs &in) {
+  if (!in.batch) return hipSuccess;
+  if (!in.kv_heads || in.heads % in.kv_heads || in.hd == 0 || in.hd > 512 || !in.capacity || !in.window)
+    return hipErrorInvalidValue;
+  AttnK a;
+  a.q = in.q; a.k = in.k; a.v = in.v; a.y = in.y; a.part = in.partial;
+  a.heads = in.heads; a.kvh = in.kv_heads; a.hd = in.hd; a.start = in.start; a.start_dev = in.start_dev;
+  a.scale = in.scale; a.window = in.window; a.capacity = in.capacity; a.batch = in.batch;
+  a.group = in.heads / in.kv_heads;
+  AttnPlan p;
+  if (!attn_plan(in, in.partial ? in.partial_floats : 0, p)) return hipErrorInvalidValue;
+  if (p.mfma_hd == 64) return launch_attn_prompt<64>(s, a, in, p.nsplit);
+  if (p.mfma_hd == 128) return launch_attn_prompt<128>(s, a, in, p.nsplit);
+  if (p.mfma_hd == 256) return launch_attn_prompt<256>(s, a, in, p.nsplit);
+  a.qb = p.qb; a.R = p.R; a.T = p.T;
+  const uint32_t qblocks = p.qblocks, nsplit = p.nsplit;
   a.nsplit = nsplit;
   size_t lds = sizeof(float) * ((size_t)a.T * (in.hd + 1) + (size_t)a.T * in.hd + (size_t)a.R * in.hd +
                                 (size_t)a.R * a.T + 3 * a.R);
-  static bool big_lds = false;
-  if (lds > 65536 && !big_lds) {
-    (void)hipFuncSetAttribute((const void *)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    big_lds = true;
-  }
+  if (lds > 65536) lds_opt_in((const void *)k_attention);
   hipLaunchKernelGGL(k_attention, dim3(in.kv_heads, qblocks, nsplit), dim3(256), lds, s, a);
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {

@@ -640,11 +640,7 @@ bool gemm_splits_input(const Matrix &w, const GemmScratch *scratch, uint32_t bat
 
 template <int T0, int T1>
 static void launch_qgemm(hipStream_t s, dim3 grid, const QGemm &q) {
-  static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
-  if (!big) {
-    (void)hipFuncSetAttribute((const void *)k_gemm_q<T0, T1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)QG_LDS);
-    big = true;
-  }
+  lds_opt_in((const void *)k_gemm_q<T0, T1>);
   hipLaunchKernelGGL((k_gemm_q<T0, T1>), grid, dim3(256), QG_LDS, s, q);
 }
 

@@ -174,6 +174,9 @@ struct AttnArgs {
   uint16_t *xs = nullptr; bool *xs_written = nullptr;
 };
 hipError_t attention(hipStream_t s, const AttnArgs &a);
+// Floats of split-K partials attention() writes for these arguments when its scratch does
+// not limit the split count (0: one split, no scratch used).
+uint64_t attention_partial_need(const AttnArgs &a);
 uint64_t attention_scratch_floats(uint32_t heads, uint32_t hd, uint32_t batch, uint32_t max_keys);
 hipError_t add(hipStream_t s, const float *delta, float *state, uint32_t n);
 hipError_t glu(hipStream_t s, const float *gate, const float *up, float *y, uint32_t n, int act);
@@ -193,6 +196,10 @@ hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *st
                     float eps, uint32_t batch);
 
 int device_cu_count();
+// Lets `kernel` take dynamic LDS up to the CU's 160 KB (the default limit is 64 KB): set
+// once per kernel (each template instance is its own kernel), before its first launch.
+void lds_opt_in(const void *kernel);
+constexpr uint32_t LDS_MAX = 160 * 1024;
 
 }  // namespace wgd
 

@@ -701,7 +701,7 @@ bool mv_mixable(int a, int b) {
   return (a == Q4_K || a == Q5_K) && b == Q6_K;
 }
 
-static uint32_t lds_limit() { return 160 * 1024; }
+static uint32_t lds_limit() { return LDS_MAX; }
 
 uint32_t mv_arg_entries(const Matrix &w) {
   const MVPlan p = mv_plan(w, &w.rows, 1, false, false);
@@ -778,11 +778,7 @@ template <class T0, class T1, bool GLU>
 static hipError_t launch_t(hipStream_t s, const MV &m, const MVPlan &p) {
   const dim3 grid(p.tiles), block(p.threads);
   auto go = [&](auto kernel) -> hipError_t {
-    static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
-    if (p.lds > 64 * 1024 && !big) {
-      (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit());
-      big = true;
-    }
+    if (p.lds > 64 * 1024) lds_opt_in((const void *)kernel);
     hipLaunchKernelGGL(kernel, grid, block, p.lds, s, m);
     return hipGetLastError();
   };
@@ -831,11 +827,7 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
       m.arg_part = out->arg_part;
     }
     auto go = [&](auto kernel) -> hipError_t {
-      static bool big = false;  // opt in above the default dynamic LDS limit once per kernel
-      if (p.lds > 64 * 1024 && !big) {
-        (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit());
-        big = true;
-      }
+      if (p.lds > 64 * 1024) lds_opt_in((const void *)kernel);
       hipLaunchKernelGGL(kernel, dim3(p.tiles), dim3(MV16_THREADS), p.lds, s, m);
       return hipGetLastError();
     };

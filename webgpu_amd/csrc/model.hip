@@ -809,6 +809,9 @@ int wgd_model_forward(wgd_model *m, const int32_t *ids, int32_t n, int32_t start
   hipSetDevice(ctx->device);
   if (!m->ready) return fail(ctx, WGD_E_STATE, "Load a model first.");
   if (!ids || n < 1 || n > m->c.batch || start < 0) return fail(ctx, WGD_E_INVALID, "forward: %d tokens at %d (batch %d)", n, start, m->c.batch);
+  // positions past the context would wrap the full-context rings onto live keys
+  if ((int64_t)start + n > m->c.context)
+    return fail(ctx, WGD_E_INVALID, "forward: positions %d..%d outside the context of %d", start, start + n - 1, m->c.context);
   int rc = validate_ids(m, ids, n);
   if (rc) return rc;
   hipStream_t s = ctx->stream;

@@ -8,6 +8,9 @@
 // The activation row is staged once per workgroup in LDS together with its 32- or
 // 16-element partial sums, so the affine Q4_K minimum and the Q6_K/Q8_0 offsets are
 // applied once per sub-block: sum_j (d*sc*q_j - dmin*m) x_j = d*sc*sum_j q_j x_j - dmin*m*sum_j x_j.
+#include <mutex>
+#include <unordered_set>
+
 #include "internal.h"
 #include "decode.h"
 #include "model.h"
@@ -333,6 +336,14 @@ int device_cu_count() {
     if (g_cus <= 0) g_cus = 256;
   }
   return g_cus;
+}
+
+void lds_opt_in(const void *kernel) {
+  static std::mutex mu;
+  static std::unordered_set<const void *> done;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.insert(kernel).second)
+    (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
 }
 
 hipError_t matmul(hipStream_t s, const Matrix &w, const float *x, float *y, uint32_t stride,

@@ -229,7 +229,8 @@ int wgd_read(wgd_context *ctx, const wgd_buffer *b, uint64_t offset, void *out, 
 int wgd_copy(wgd_context *ctx, const wgd_buffer *src, wgd_buffer *dst, uint64_t size, uint64_t so, uint64_t dof) {
   NEED_CTX(ctx); NEED_BUF(ctx, src, "wgd_copy"); NEED_BUF(ctx, dst, "wgd_copy");
   if (!size) return WGD_OK;
-  if (so + size > src->size || dof + size > dst->size) return fail(ctx, WGD_E_INVALID, "wgd_copy: range outside buffers");
+  if (so > src->size || size > src->size - so || dof > dst->size || size > dst->size - dof)
+    return fail(ctx, WGD_E_INVALID, "wgd_copy: range outside buffers");
   return ctx_check(ctx, hipMemcpyAsync((uint8_t *)dst->ptr + dof, (const uint8_t *)src->ptr + so, size, hipMemcpyDeviceToDevice, ctx->stream), "wgd_copy");
 }
 
@@ -385,32 +386,44 @@ int wgd_rope_adjacent(wgd_context *ctx, wgd_buffer *x, uint32_t heads, uint32_t 
   return rope_common(ctx, x, nullptr, heads, hd, start, theta, scale, 0.f, rot, batch, 2);
 }
 
-int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, const wgd_buffer *v, wgd_buffer *y,
-                  uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t start, float scale, uint32_t window,
-                  uint32_t capacity, uint32_t context, uint32_t batch) {
-  NEED_CTX(ctx); NEED_BUF(ctx, q, "attention"); NEED_BUF(ctx, k, "attention"); NEED_BUF(ctx, v, "attention"); NEED_BUF(ctx, y, "attention");
+// The checks and arguments shared by both attention entry points (partial left unset).
+static int attention_args(wgd_context *ctx, const char *what, const wgd_buffer *q, const wgd_buffer *k,
+                          const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                          uint32_t start, float scale, uint32_t window, uint32_t capacity, uint32_t context,
+                          uint32_t batch, AttnArgs &a) {
+  NEED_BUF(ctx, q, what); NEED_BUF(ctx, k, what); NEED_BUF(ctx, v, what); NEED_BUF(ctx, y, what);
   uint32_t cap = capacity ? capacity : context;
   if (!kv_heads || !heads || heads % kv_heads || !hd || hd > 512 || !cap || !window)
-    return fail(ctx, WGD_E_INVALID, "attention: invalid heads %u/%u, head_dim %u, capacity %u or window %u", heads, kv_heads, hd, cap, window);
-  if ((heads / kv_heads) > 16) return fail(ctx, WGD_E_INVALID, "attention: more than 16 query heads per KV head");
-  if (!batch) return WGD_OK;
+    return fail(ctx, WGD_E_INVALID, "%s: invalid heads %u/%u, head_dim %u, capacity %u or window %u", what, heads, kv_heads, hd, cap, window);
+  if ((heads / kv_heads) > 16) return fail(ctx, WGD_E_INVALID, "%s: more than 16 query heads per KV head", what);
   NEED_FIT(ctx, q, (uint64_t)batch * heads * hd * 4, "attention queries");
   NEED_FIT(ctx, k, (uint64_t)cap * kv_heads * hd * 4, "attention keys");
   NEED_FIT(ctx, v, (uint64_t)cap * kv_heads * hd * 4, "attention values");
   NEED_FIT(ctx, y, (uint64_t)batch * heads * hd * 4, "attention output");
+  a = AttnArgs{};
+  a.q = (const float *)q->ptr; a.k = (const float *)k->ptr; a.v = (const float *)v->ptr; a.y = (float *)y->ptr;
+  a.heads = heads; a.kv_heads = kv_heads; a.hd = hd; a.start = start; a.start_dev = nullptr;
+  a.scale = scale; a.window = window; a.capacity = cap; a.batch = batch;
+  a.partial = nullptr; a.partial_floats = 0;
+  return WGD_OK;
+}
+
+int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, const wgd_buffer *v, wgd_buffer *y,
+                  uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t start, float scale, uint32_t window,
+                  uint32_t capacity, uint32_t context, uint32_t batch) {
+  NEED_CTX(ctx);
+  AttnArgs a;
+  int rc = attention_args(ctx, "attention", q, k, v, y, heads, kv_heads, hd, start, scale, window, capacity, context, batch, a);
+  if (rc || !batch) return rc;
   uint64_t need = attention_scratch_floats(heads, hd, batch, (uint32_t)device_cu_count() * 4);
   if (need > ctx->att_partial_floats) {
     ctx_free(ctx, ctx->att_partial);
     ctx->att_partial = nullptr; ctx->att_partial_floats = 0;
     void *p = nullptr;
-    int rc = ctx_alloc(ctx, need * 4, "attention split scratch", &p);
+    rc = ctx_alloc(ctx, need * 4, "attention split scratch", &p);
     if (rc) return rc;
     ctx->att_partial = (float *)p; ctx->att_partial_floats = need;
   }
-  AttnArgs a;
-  a.q = (const float *)q->ptr; a.k = (const float *)k->ptr; a.v = (const float *)v->ptr; a.y = (float *)y->ptr;
-  a.heads = heads; a.kv_heads = kv_heads; a.hd = hd; a.start = start; a.start_dev = nullptr;
-  a.scale = scale; a.window = window; a.capacity = cap; a.batch = batch;
   a.partial = ctx->att_partial; a.partial_floats = (uint32_t)(ctx->att_partial_floats > 0xFFFFFFFFull ? 0xFFFFFFFFull : ctx->att_partial_floats);
   return ctx_check(ctx, attention(ctx->stream, a), "attention");
 }

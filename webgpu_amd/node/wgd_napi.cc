@@ -17,7 +17,7 @@
 namespace {
 
 struct Ctx { wgd_context *ctx = nullptr; };
-struct Model { wgd_model *m = nullptr; Ctx *owner = nullptr; };
+struct Model { wgd_model *m = nullptr; Ctx *owner = nullptr; int32_t vocab = 0; };
 
 napi_value undefined(napi_env env) {
   napi_value u;
@@ -186,7 +186,7 @@ napi_value model_create(napi_env env, napi_callback_info info) {
     return throw_msg(env, "WGD_E_INVALID", "capacities must be an Int32Array with one entry per layer");
   wgd_model *m = nullptr;
   CHECK(c->ctx, wgd_model_create(c->ctx, &cfg, (const int32_t *)caps, &m));
-  Model *w = new Model{m, c};
+  Model *w = new Model{m, c, cfg.vocab};
   return make_external(env, w, [](napi_env, void *p, void *) { delete (Model *)p; });
 }
 
@@ -250,6 +250,10 @@ napi_value model_forward(napi_env env, napi_callback_info info) {
   size_t nl = 0;
   if (vt != napi_null && vt != napi_undefined && !typed(env, argv[3], napi_float32_array, &logits, &nl))
     return throw_msg(env, "WGD_E_INVALID", "logits must be a Float32Array or null");
+  // the library writes vocab floats into it
+  if (logits && nl < (size_t)w->vocab)
+    return throw_msg(env, "WGD_E_INVALID", "logits holds " + std::to_string(nl) + " floats, the vocabulary " +
+                                               std::to_string(w->vocab));
   int32_t tok = -1;
   CHECK(w->owner->ctx, wgd_model_forward(w->m, (const int32_t *)ids, (int32_t)n, start, (float *)logits, &tok));
   napi_value r;

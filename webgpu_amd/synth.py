@@ -160,6 +160,12 @@ SPECS: Dict[str, Spec] = {
                       {"embd": Q4_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K}, context_length=8192),
     "gemma3-27b": Spec("gemma3-27b", "gemma3", 62, 5376, 32, 16, 128, 21504, 262144, 1e-6, 1_000_000.0, True, True,
                        {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K}, context_length=131072),
+    # The Gemma-3-27B widths at six layers: five local (window 1024) and one global layer
+    # (period 6), so a prompt past 1151 tokens wraps the local rings inside the model. At
+    # this depth modelConfig takes the attention scale 1/sqrt(head_dim) (gguf.ts:134).
+    "gemma3-27b-6l": Spec("gemma3-27b-6l", "gemma3", 6, 5376, 32, 16, 128, 21504, 262144, 1e-6, 1_000_000.0, True,
+                          True, {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K},
+                          context_length=131072),
 }
 
 
