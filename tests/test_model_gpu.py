@@ -1,11 +1,12 @@
 """End-to-end token-loop parity on the MI355X: the native decoder vs the float64 oracle.
 
 Contract (the runtime's parity bar): logits within 1e-3 max-relative error
-(max|got - want| / max|want|) and greedy tokens identical. Every step also reports the
-oracle's top-2 margin, as scripts/verify-dense.mjs:209-210 does; a step whose margin is
-below the logits tolerance could legitimately flip, and the test says so instead of
-passing silently. Greedy steps are teacher-forced on the oracle's tokens so one flip
-cannot cascade.
+(max|got - want| / max|want|) and greedy tokens identical, with no exception for small
+margins. The whole workloads (the prompt in 128-token batches, then free-running greedy
+tokens from the device decode loop) are checked against fixtures the oracle wrote
+(tests/golden/make_model_goldens.py, run in the build container: the f64 oracle needs
+tens of minutes for the 8B shape). Every fixture step's top-2 margin clears the logits
+tolerance, so identical tokens are a fair demand (scripts/verify-dense.mjs:281-286,304).
 """
 import os
 
@@ -54,15 +55,15 @@ def check_model(name, prompt_len, steps, context=512, chunk=128, seed=7):
             tok = int(np.argmax(want))
             margins.append(float(want[order[0]] - want[order[1]]))
             gtok = int(np.argmax(got))
-            assert gtok == tok or margins[-1] < LOGIT_TOL * np.abs(want).max(), \
-                f"{name} step {s}: GPU token {gtok} vs oracle {tok} (margin {margins[-1]:.3e})"
+            assert gtok == tok, f"{name} step {s}: GPU token {gtok} vs oracle {tok} (margin {margins[-1]:.3e})"
             toks.append(tok)
             if s + 1 < steps:
                 want = ora.forward([tok], pos)
                 got = eng.forward([tok], pos, True)
                 errs.append(max_rel(got, want))
                 pos += 1
-        print(f"\n{name}: max-rel logits error {max(errs):.3e}, min top-2 margin {min(margins):.3e}, tokens {toks[:8]}")
+        print(f"\n{name}: max-rel logits error {max(errs):.3e}, min top-2 margin {min(margins):.3e}, tokens {toks[:8]}",
+              flush=True)
         assert max(errs) <= LOGIT_TOL, f"{name}: logits max-rel error {max(errs):.3e}"
         return eng, ora, ids, toks
     except BaseException:
@@ -114,19 +115,121 @@ def test_prefix_reuse_across_turns():
         eng.dispose()
 
 
-def test_qwen3_0_6b_shape():
-    eng, *_ = check_model("qwen3-0.6b", 64, 12, context=1024)
+def test_forward_rejects_positions_past_the_context():
+    f, g, c, caps, eng = build("tiny", 512, batch=8)
+    try:
+        with pytest.raises(Exception, match="outside the context"):
+            eng.forward([1, 2, 3, 4], 510, True)
+        with pytest.raises(Exception, match="exceed"):
+            eng.decode(1, 500, 20)
+        eng.forward([1, 2], 510, True)  # positions 510 and 511 are the last two
+    finally:
+        eng.dispose()
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load_fixture(name):
+    import xxhash
+    z = np.load(os.path.join(GOLDEN, f"model_{name}.npz"), allow_pickle=False)
+    f = synth.build(name)
+    assert xxhash.xxh64(memoryview(f)).hexdigest() == str(z["gguf_xxh64"]), \
+        f"{name}: the synthetic GGUF differs from the one the fixture was made from"
+    return f, z
+
+
+def run_workload(name):
+    """The fixture's workload through the engine: prompt batches of 128 (the last one with
+    logits), the device decode loop for all but the last step, then one eager step whose
+    logits are the fixture's last ones."""
+    f, z = load_fixture(name)
+    g = parse_gguf_header(f, f.size)
+    c = model_config(g)
+    context, chunk = int(z["context"]), int(z["chunk"])
+    prompt, want = [int(t) for t in z["prompt"]], [int(t) for t in z["tokens"]]
+    eng = PagedEngine()
+    eng.load(f, LoadOptions(contextLength=context, batchSize=chunk))
+    try:
+        n = len(prompt)
+        for i in range(0, n, chunk):
+            part = prompt[i:i + chunk]
+            got = eng.forward(part, i, i + len(part) == n)
+        e_first = max_rel(got, z["first_logits"])
+        first = int(np.argmax(got))
+        assert first == want[0], f"{name}: first token {first} vs oracle {want[0]}"
+        steps = len(want)
+        toks = [first]
+        if steps > 2:
+            toks += eng.decode(first, n, steps - 2)   # feeds want[0..steps-3]
+        last = eng.forward([toks[-1]], n + steps - 2, True) if steps > 1 else got
+        e_last = max_rel(last, z["last_logits"])
+        if steps > 1:
+            toks.append(int(np.argmax(last)))
+        rel = z["margins"] / z["maxabs"]
+        diff = [i for i, (a, b) in enumerate(zip(toks, want)) if a != b]
+        print(f"\n{name}: prompt {n} (seed {int(z['prompt_seed'])}), {steps} greedy tokens; logits max-rel "
+              f"{e_first:.2e} after the prompt, {e_last:.2e} at the last step; min oracle margin {rel.min():.2e} "
+              f"of max|logit|; first differing step {diff[0] if diff else None}", flush=True)
+        assert toks == want, f"{name}: greedy tokens differ from step {diff[0]}: {toks[diff[0]]} vs {want[diff[0]]}"
+        assert e_first <= LOGIT_TOL and e_last <= LOGIT_TOL, (e_first, e_last)
+        return eng, z
+    except BaseException:
+        eng.dispose()
+        raise
+
+
+def test_qwen3_0_6b_full_workload():
+    """64-token prompt, 256 free-running greedy tokens."""
+    eng, _ = run_workload("qwen3-0.6b")
     eng.dispose()
 
 
 @pytest.mark.slow
-def test_llama3_8b_shape_prompt_gemm_and_decode():
-    # 136-token prompt: one 128-token MFMA GEMM chunk plus an 8-token chunk, then decode.
-    eng, *_ = check_model("llama3-8b", 136, 5, context=1024)
+def test_llama3_8b_full_workload():
+    """512-token prompt in four 128-token batches (the MFMA prompt GEMM), then 256
+    free-running greedy tokens: the workload whose tokens must equal the reference's."""
+    eng, _ = run_workload("llama3-8b")
     eng.dispose()
+
+
+@pytest.mark.slow
+def test_gemma3_full_width_local_rings_wrap():
+    """Gemma-3-27B widths at six layers (five local, one global): a 1280-token prompt in ten
+    batches wraps the 1151-slot local rings inside the model, then 32 greedy tokens."""
+    eng, z = run_workload("gemma3-27b-6l")
+    try:
+        assert min(eng.kvCapacities) == 1151 and int(z["prompt_len"]) > 1151
+    finally:
+        eng.dispose()
 
 
 @pytest.mark.slow
 def test_gemma3_27b_shape_local_and_global_layers():
+    """All 62 layers against the oracle at a short prompt (logits and tokens)."""
     eng, *_ = check_model("gemma3-27b", 24, 3, context=2048)
     eng.dispose()
+
+
+@pytest.mark.slow
+def test_gemma3_27b_8k_context_properties():
+    """All 62 layers at the 8192-token prompt of the Gemma workload (64 batches of 128): the
+    logits are finite, the graph decode loop equals eager steps for 16 tokens, and a replay
+    from the same state repeats them."""
+    f, g, c, caps, eng = build("gemma3-27b", 8448)
+    try:
+        ids = synth.prompt_ids(c.vocab, 8192, 7)
+        for i in range(0, 8192, 128):
+            logits = eng.forward(ids[i:i + 128], i, i + 128 == 8192)
+        assert np.isfinite(logits).all()
+        first = int(np.argmax(logits))
+        dev = eng.decode(first, 8192, 16)
+        eager, tok = [], first
+        for i in range(16):
+            tok = eng.forward_argmax([tok], 8192 + i)
+            eager.append(tok)
+        assert dev == eager
+        assert eng.decode(first, 8192, 16) == dev
+        print(f"\ngemma3-27b 8K: tokens {dev}", flush=True)
+    finally:
+        eng.dispose()
