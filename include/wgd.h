@@ -143,6 +143,19 @@ int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k,
                   const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads,
                   uint32_t head_dim, uint32_t start, float scale, uint32_t window,
                   uint32_t capacity, uint32_t context, uint32_t batch);
+/* wgd_attention with no allocation: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and the same results, bit for bit: the
+ * split-K partials go to a static array in the library's device memory (one per GPU, held
+ * until the process ends) instead of context scratch. Sizes whose partials exceed
+ * wgd_attention_noalloc_limit() floats fail with WGD_E_INVALID. Calls on one GPU share the
+ * array: calls that overlap on one GPU (two streams) race. */
+int wgd_attention_noalloc(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k,
+                          const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads,
+                          uint32_t head_dim, uint32_t start, float scale, uint32_t window,
+                          uint32_t capacity, uint32_t context, uint32_t batch);
+/* Floats of the static scratch of wgd_attention_noalloc (8 Mi floats, 32 MiB). */
+uint64_t wgd_attention_noalloc_limit(void);
 /* addShader (shaders.ts:123-128): state += delta. */
 int wgd_add(wgd_context *ctx, const wgd_buffer *delta, wgd_buffer *state, uint32_t n);
 /* siluShader (qwen-shaders.ts:27-34): y = g / (1 + exp(-g)) * up. */

@@ -21,6 +21,7 @@ struct wgd_context {
   int32_t *argmax_scratch = nullptr;  // int32 result + 256 partial keys
   float *att_partial = nullptr;       // split-K scratch of the per-kernel attention launcher
   uint64_t att_partial_floats = 0;
+  float *noalloc_scratch = nullptr;  // this device's static scratch (wgd_attention_noalloc)
   void *mv_qx = nullptr;              // quantized activation row of wgd_matmul
   uint64_t mv_qx_bytes = 0;
   float *gemm_part = nullptr;         // split-K partial sums of wgd_matmul's prompt GEMM

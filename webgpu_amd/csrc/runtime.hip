@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdarg>
 #include <cstring>
+#include <mutex>
 #include <set>
 #include <string>
 
@@ -29,6 +30,7 @@ struct wgd_buffer {
 };
 
 static thread_local std::string g_error;
+static int scratch_setup(int device, float **out);
 
 int wgd::fail(wgd_context *ctx, int code, const char *fmt, ...) {
   char buf[1024];
@@ -104,8 +106,12 @@ int wgd_create(int32_t device, uint64_t budget_bytes, wgd_context **out) {
   if (e != hipSuccess) return fail(nullptr, WGD_E_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
   if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
     return fail(nullptr, WGD_E_DEVICE, "libwgd is built for gfx950 (MI355X); device %d is %s.", device, p.gcnArchName);
+  float *static_scratch = nullptr;
+  int src = scratch_setup(device, &static_scratch);
+  if (src) return src;
   wgd_context *ctx = new wgd_context();
   ctx->device = device;
+  ctx->noalloc_scratch = static_scratch;
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) { delete ctx; return fail(nullptr, WGD_E_DEVICE, "hipStreamCreate: %s", hipGetErrorString(e)); }
   size_t free_b = 0, total_b = 0;
@@ -427,6 +433,60 @@ int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, co
   a.partial = ctx->att_partial; a.partial_floats = (uint32_t)(ctx->att_partial_floats > 0xFFFFFFFFull ? 0xFFFFFFFFull : ctx->att_partial_floats);
   return ctx_check(ctx, attention(ctx->stream, a), "attention");
 }
+
+// ---------------------------------------------------------------- allocation-free attention
+// The split-K partials of wgd_attention_noalloc live in this array of the library's own
+// device memory: each GPU the library runs on holds one copy until the process ends, so the
+// entry point calls no allocator. In host code `scratch` names a host-side stand-in, never
+// device memory: its address on each GPU comes from hipGetSymbolAddress, taken once per
+// device by wgd_create with that device current, and only that address reaches kernels.
+// Calls on one GPU share its copy (overlapping calls from two streams race); every split
+// writes each of its partial rows before the merge reads them, so nothing needs clearing.
+static constexpr uint64_t NOALLOC_SCRATCH_FLOATS = 8ull << 20;  // 32 MiB
+static __device__ __attribute__((used)) __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
+static constexpr int SCRATCH_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static float *g_scratch_ptr[SCRATCH_DEVICES];
+
+// The device address of `scratch` on the current device `device` (once per device).
+static int scratch_setup(int device, float **out) {
+  if (device < 0 || device >= SCRATCH_DEVICES)
+    return fail(nullptr, WGD_E_DEVICE, "device %d is beyond the %d devices the static scratch covers", device, SCRATCH_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(nullptr, WGD_E_DEVICE, "static scratch address on device %d: %s", device, hipGetErrorString(e));
+    g_scratch_ptr[device] = (float *)ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return WGD_OK;
+}
+
+int wgd_attention_noalloc(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, const wgd_buffer *v,
+                          wgd_buffer *y, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t start, float scale,
+                          uint32_t window, uint32_t capacity, uint32_t context, uint32_t batch) {
+  NEED_CTX(ctx);
+  AttnArgs a;
+  int rc = attention_args(ctx, "attention_noalloc", q, k, v, y, heads, kv_heads, hd, start, scale, window, capacity,
+                          context, batch, a);
+  if (rc || !batch) return rc;
+  if (!ctx->noalloc_scratch) return fail(ctx, WGD_E_STATE, "attention_noalloc: no static scratch on device %d", ctx->device);
+  // the split plan of wgd_attention, whose scratch never limits it: the same launches and
+  // the same partial sums, so both entry points give the same bits
+  const uint64_t need = attention_partial_need(a);
+  if (need > NOALLOC_SCRATCH_FLOATS)
+    return fail(ctx, WGD_E_INVALID,
+                "attention_noalloc: %u tokens x %u heads x head_dim %u need %llu floats of split scratch; the static "
+                "scratch holds %llu (use wgd_attention or a smaller batch)",
+                batch, heads, hd, (unsigned long long)need, (unsigned long long)NOALLOC_SCRATCH_FLOATS);
+  a.partial = ctx->noalloc_scratch;
+  a.partial_floats = (uint32_t)need;
+  return ctx_check(ctx, attention(ctx->stream, a), "attention_noalloc");
+}
+
+uint64_t wgd_attention_noalloc_limit(void) { return NOALLOC_SCRATCH_FLOATS; }
 
 int wgd_add(wgd_context *ctx, const wgd_buffer *delta, wgd_buffer *state, uint32_t n) {
   NEED_CTX(ctx); NEED_BUF(ctx, delta, "add"); NEED_BUF(ctx, state, "add");

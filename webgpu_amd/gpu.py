@@ -48,6 +48,8 @@ SIGNATURES = {
     "wgd_rope_neox": (C.c_int, [_P, _P, _U32, _U32, _U32, _F, _F, _U32, _U32]),
     "wgd_rope_adjacent": (C.c_int, [_P, _P, _U32, _U32, _U32, _F, _F, _U32, _U32]),
     "wgd_attention": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
+    "wgd_attention_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
+    "wgd_attention_noalloc_limit": (_U64, []),
     "wgd_add": (C.c_int, [_P, _P, _P, _U32]),
     "wgd_silu": (C.c_int, [_P, _P, _P, _P, _U32]),
     "wgd_gelu": (C.c_int, [_P, _P, _P, _P, _U32]),
@@ -240,6 +242,13 @@ class Compute:
                   start: int, scale: float, window: int, capacity: int, context: int, batch: int = 1) -> None:
         self.check(lib().wgd_attention(self.ctx, q.ptr, k.ptr, v.ptr, y.ptr, heads, kv_heads, hd, start, scale,
                                        window, capacity, context, batch))
+
+    def attention_noalloc(self, q: Buffer, k: Buffer, v: Buffer, y: Buffer, heads: int, kv_heads: int, hd: int,
+                          start: int, scale: float, window: int, capacity: int, context: int, batch: int = 1) -> None:
+        """attention() with its split-K scratch in the library's static device array: no
+        allocation (for graph capture and allocation-free callers)."""
+        self.check(lib().wgd_attention_noalloc(self.ctx, q.ptr, k.ptr, v.ptr, y.ptr, heads, kv_heads, hd, start,
+                                               scale, window, capacity, context, batch))
 
     def add(self, delta: Buffer, state: Buffer, n: int) -> None:
         self.check(lib().wgd_add(self.ctx, delta.ptr, state.ptr, n))
