@@ -155,6 +155,40 @@ def matvec_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, lau
             "copies": copies}
 
 
+PROBE_CONFIGS = [(256, 512, 8), (512, 256, 8), (512, 512, 4), (1024, 256, 4), (256, 1024, 4), (1024, 512, 4)]
+
+
+def probe_bench(gpu: Compute, ev: Events, nbytes: int, out_floats: int = 0, launches: int = 96) -> dict:
+    """The per-launch floor of reading `nbytes` once (wgd_probe_read): a plain streaming read
+    of 16-byte loads rotating over copies totalling ~900 MB (beyond the Infinity Cache), best
+    of a few grid shapes, timed like the matvec (a HIP event pair around back-to-back
+    launches, which the library issues itself). With out_floats it also stores a result
+    vector of that length, as a matvec stores its rows."""
+    stride = (nbytes + 4095) // 4096 * 4096
+    copies = max(2, min(96, int(900e6 // nbytes) + 1))
+    src = gpu.buffer(copies * stride, "probe src")
+    out = gpu.buffer(max(4, out_floats * 4), "probe out")
+    best = None
+    evs = ev.create(2)
+    for wgs, threads, depth in PROBE_CONFIGS:
+        gpu.probe_read(src, nbytes, copies, copies, wgs, threads, depth, out, out_floats)
+        gpu.done()
+        times = []
+        for rep in range(3):
+            ev.record(evs[0], gpu.stream)
+            gpu.probe_read(src, nbytes, copies, launches, wgs, threads, depth, out, out_floats)
+            ev.record(evs[1], gpu.stream)
+            times.append(ev.elapsed_ms(evs[0], evs[1]) * 1e-3 / launches)
+        t = float(np.mean(times))
+        if best is None or t < best["us"] * 1e-6:
+            best = {"bytes": nbytes, "out_floats": out_floats, "us": t * 1e6, "GBps": nbytes / t / 1e9,
+                    "frac": nbytes / t / PEAK_HBM, "grid": f"{wgs}x{threads} depth {depth}"}
+    ev.destroy(evs)
+    gpu.destroy(src)
+    gpu.destroy(out)
+    return best
+
+
 PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA peak, flop/s
 GEMM_SHAPES = [(Q4_K, 4096, 14336, 128), (Q4_K, 14336, 4096, 128), (Q4_K, 4096, 4096, 128), (Q6_K, 4096, 1024, 128)]
 
@@ -222,6 +256,9 @@ def main() -> None:
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the matvec microbench and a 256 MiB device copy (counter calibration), no JSON line")
     ap.add_argument("--gemm-only", action="store_true", help="only the prompt-GEMM microbench, no JSON line")
+    ap.add_argument("--probe", action="store_true",
+                    help="only the plain-read probe (the per-launch read floor) at the matvec byte counts, with and "
+                         "without a result store; one JSON line per case")
     ap.add_argument("--sample-only", action="store_true",
                     help="only the device sampler (T 0.7, top-k 40, top-p 0.9) on normal logits rows of three vocabulary "
                          "sizes, 30 draws each, no JSON line")
@@ -248,6 +285,18 @@ def main() -> None:
             m = matvec_bench(gpu, ev, *s)
             print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
                   f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+        gpu.dispose()
+        return
+    if a.probe:
+        gpu = Compute().init()
+        ev = Events()
+        # the Q4_K weight bytes of 4096x4096 and of 14336x4096 / 4096x14336, and a 66 MB pair
+        for nbytes, rows in ((9437184, 4096), (33030144, 4096), (33030144, 14336), (66060288, 14336)):
+            for out_floats in (0, rows):
+                r = probe_bench(gpu, ev, nbytes, out_floats)
+                print(json.dumps({"probe": r}), flush=True)
+                print(f"[bench] probe {nbytes} B, {out_floats} result floats: {r['us']:.2f} us, {r['GBps']:.0f} GB/s "
+                      f"({100 * r['frac']:.1f}% of 8 TB/s) at {r['grid']}", file=sys.stderr, flush=True)
         gpu.dispose()
         return
     if a.sample_only:
@@ -354,6 +403,9 @@ def main() -> None:
         shapes = [(Q4_K, 14336, 4096), (Q4_K, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 4096, 128256)]
         mv = [matvec_bench(gpu, ev, *s) for s in shapes]
         gm = [gemm_bench(gpu, ev, *sh) for sh in GEMM_SHAPES]
+        # the plain-read floor for the same weight bytes, with the matvec's result store
+        pr = {m["shape"]: probe_bench(gpu, ev, m["bytes"] - 4 * int(m["shape"].split("x")[0]) - 4 * int(m["shape"].split("x")[1]),
+                                      int(m["shape"].split("x")[1])) for m in mv[:3]}
         gpu.dispose()
         head = mv[0]
         result["roofline"] = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
@@ -361,6 +413,10 @@ def main() -> None:
                               "kernel": f"k_matvec<Q4K> {head['shape']} (in x out), {head['bytes']} B per launch",
                               "mean_us": head["us"]}
         result["matvec"] = mv
+        result["probe"] = [{"shape": k, "read_us": v["us"], "read_frac": v["frac"], "grid": v["grid"],
+                            "matvec_us": next(m["us"] for m in mv if m["shape"] == k),
+                            "matvec_over_probe": next(m["us"] for m in mv if m["shape"] == k) / v["us"]}
+                           for k, v in pr.items()]
         result["prefill_gemm"] = gm
         for m in mv:
             print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "

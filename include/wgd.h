@@ -188,6 +188,18 @@ int wgd_sample(wgd_context *ctx, const wgd_buffer *logits, uint32_t n, double te
 int wgd_embed(wgd_context *ctx, int32_t type, const wgd_buffer *table, const wgd_buffer *ids,
               wgd_buffer *out, uint32_t hidden, uint32_t n, double scale);
 
+/* ---------------------------------------------------------------- measurement
+ * No reference counterpart: `launches` back-to-back plain streaming reads of `bytes`
+ * (multiple of 16), launch i reading copy i % copies of src (copies laid out `bytes`
+ * rounded up to 4 KiB apart), by `workgroups` workgroups of `threads` threads with `depth`
+ * (4, 8, 16) 16-byte loads in flight per lane, a contiguous range per workgroup. With
+ * out_floats > 0 each workgroup also stores its share of an out_floats-long result into
+ * out. It is the per-launch floor of a kernel that reads those bytes once (bench.py
+ * --probe); the loop runs in the library so the host does not pace short launches. */
+int wgd_probe_read(wgd_context *ctx, const wgd_buffer *src, uint64_t bytes, uint32_t copies,
+                   uint32_t launches, uint32_t workgroups, uint32_t threads, uint32_t depth,
+                   wgd_buffer *out, uint32_t out_floats);
+
 /* ---------------------------------------------------------------- model
  * The dense decoder step (engine.ts:138-180, 217-251) with resident weights. */
 

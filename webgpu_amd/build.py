@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libwgd.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["runtime.hip", "quant.hip", "matvec.hip", "gemm.hip", "ops.hip", "attention.hip", "model.hip", "sample.hip"]
+SOURCES = ["runtime.hip", "quant.hip", "matvec.hip", "gemm.hip", "ops.hip", "attention.hip", "model.hip", "sample.hip", "probe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",

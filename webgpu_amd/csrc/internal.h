@@ -196,6 +196,10 @@ hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *st
                     float eps, uint32_t batch);
 
 int device_cu_count();
+// A plain streaming read of bytes (multiple of 16) by wgs workgroups of `threads`, depth
+// 16-byte loads in flight per lane; out_n > 0 also stores an out_n-float result.
+hipError_t probe_read(hipStream_t s, const uint8_t *p, uint32_t bytes, uint32_t wgs, uint32_t threads, uint32_t depth,
+                      float *out, uint32_t out_n);
 // Lets `kernel` take dynamic LDS up to the CU's 160 KB (the default limit is 64 KB): set
 // once per kernel (each template instance is its own kernel), before its first launch.
 void lds_opt_in(const void *kernel);

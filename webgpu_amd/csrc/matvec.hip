@@ -390,6 +390,12 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
     xsm[j] = bl4c(rxm, i);
     xsq[j] = bl4c(rxq, i);
   }
+  // A CU returns load data in request order, so a wavefront that started late would find its
+  // activation requests behind the other wavefronts' weight requests: a bare barrier (no
+  // wait for data) puts every wavefront's activation requests ahead of all weight requests.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int d = 0; d < DU; d++) issue(d);
   __builtin_amdgcn_sched_barrier(0);

@@ -434,6 +434,28 @@ int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, co
   return ctx_check(ctx, attention(ctx->stream, a), "attention");
 }
 
+int wgd_probe_read(wgd_context *ctx, const wgd_buffer *src, uint64_t bytes, uint32_t copies, uint32_t launches,
+                   uint32_t workgroups, uint32_t threads, uint32_t depth, wgd_buffer *out, uint32_t out_floats) {
+  NEED_CTX(ctx); NEED_BUF(ctx, src, "probe_read");
+  const uint64_t stride = (bytes + 4095) / 4096 * 4096;
+  if (!bytes || bytes % 16 || bytes >= (1ull << 31) || !copies || !launches || copies * stride > src->size || !workgroups ||
+      !threads || threads % 64 || threads > 1024 || (depth != 4 && depth != 8 && depth != 16))
+    return fail(ctx, WGD_E_INVALID, "probe_read: %llu bytes (multiple of 16, < 2 GiB) x %u copies within the buffer, "
+                "%u launches, %u workgroups of %u threads (multiple of 64, <= 1024), depth %u (4, 8 or 16)",
+                (unsigned long long)bytes, copies, launches, workgroups, threads, depth);
+  if (out_floats) {
+    NEED_BUF(ctx, out, "probe_read");
+    NEED_FIT(ctx, out, (uint64_t)out_floats * 4, "probe_read output");
+  }
+  for (uint32_t i = 0; i < launches; i++) {
+    const uint8_t *p = (const uint8_t *)src->ptr + (uint64_t)(i % copies) * stride;
+    int rc = ctx_check(ctx, probe_read(ctx->stream, p, (uint32_t)bytes, workgroups, threads, depth,
+                                       out ? (float *)out->ptr : nullptr, out_floats), "probe_read");
+    if (rc) return rc;
+  }
+  return WGD_OK;
+}
+
 // ---------------------------------------------------------------- allocation-free attention
 // The split-K partials of wgd_attention_noalloc live in this array of the library's own
 // device memory: each GPU the library runs on holds one copy until the process ends, so the

@@ -50,6 +50,7 @@ SIGNATURES = {
     "wgd_attention": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
     "wgd_attention_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
     "wgd_attention_noalloc_limit": (_U64, []),
+    "wgd_probe_read": (C.c_int, [_P, _P, _U64, _U32, _U32, _U32, _U32, _U32, _P, _U32]),
     "wgd_add": (C.c_int, [_P, _P, _P, _U32]),
     "wgd_silu": (C.c_int, [_P, _P, _P, _P, _U32]),
     "wgd_gelu": (C.c_int, [_P, _P, _P, _P, _U32]),
@@ -249,6 +250,13 @@ class Compute:
         allocation (for graph capture and allocation-free callers)."""
         self.check(lib().wgd_attention_noalloc(self.ctx, q.ptr, k.ptr, v.ptr, y.ptr, heads, kv_heads, hd, start,
                                                scale, window, capacity, context, batch))
+
+    def probe_read(self, src: Buffer, nbytes: int, copies: int, launches: int, workgroups: int, threads: int,
+                   depth: int, out: Optional[Buffer] = None, out_floats: int = 0) -> None:
+        """`launches` plain streaming reads of nbytes, rotating over `copies` copies in src (the
+        per-launch read floor; measurement only)."""
+        self.check(lib().wgd_probe_read(self.ctx, src.ptr, nbytes, copies, launches, workgroups, threads, depth,
+                                        out.ptr if out is not None else None, out_floats))
 
     def add(self, delta: Buffer, state: Buffer, n: int) -> None:
         self.check(lib().wgd_add(self.ctx, delta.ptr, state.ptr, n))
