@@ -617,152 +617,233 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
   chunk_epilogue<G, HD>(a, kv, z, wm, wl, wo);
 }
 
-// The same step with everything a lane needs kept in registers: lane l holds elements
-// l + 64e of a head (half-split rotation, rot == hd: pair (i, i + hd/2) sits in one lane) or
-// EL*l + e (adjacent pairs). The projections, norm weights and rotation frequencies are
-// loaded before the position is known; the angles are formed in f64 (p * scale * f[i]) as in
-// k_rope. Each wavefront rotates the query heads itself, so no barrier precedes the keys.
-template <int EL, int G, bool ADJ>
-__global__ __launch_bounds__(256) void k_attn_fast(AttnDecK a) {
-  constexpr uint32_t HD = 64 * EL, NP = EL / 2;
+// ------------------------------------------------------------------ decode step, 16-byte lanes
+//
+// One token: a workgroup per (kv head, chunk of keys), four wavefronts. A lane holds 8
+// elements of a key row (two 16-byte pieces, elements 4s..4s+3 and HD/2 + 4s..+3 for lane
+// s of the key's LPK = HD/8 lanes), so one wavefront load instruction covers KPW = 64/LPK
+// whole key rows, and a score needs a log2(LPK)-step DPP sum over the key's lanes rather
+// than a wave-wide one. Each key slot (a group of LPK lanes) keeps its own online-softmax
+// state over the keys it visits; the slots of a wavefront merge once at the end, then the
+// wavefronts through LDS. A wavefront loads AD2_DB key iterations at once. The prologue
+// normalises and rotates the group's query heads and the new key in registers (angles in
+// f64 as in k_rope); the workgroup whose chunk holds the position writes the new key and
+// value into the ring (slot pos % capacity: the ring keeps at least the window, so no
+// other chunk of this launch reads it) and uses the fresh values for that key.
+constexpr uint32_t AD2_DB = 4;  // key iterations (KPW keys each) per wavefront load batch
+
+template <uint32_t LPK>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_mov<0xB1>(v);                       // quad xor 1
+  v += dpp_mov<0x4E>(v);                       // quad xor 2
+  if (LPK >= 8) v += dpp_mov<0x141>(v);        // half-row mirror: the other quad of 8
+  if (LPK >= 16) v += dpp_mov<0x140>(v);       // row mirror: the other 8 of 16
+  if (LPK >= 32) v += __shfl_xor(v, 16, 64);   // the other row of 32
+  return v;
+}
+
+// Sum / max over the key slots of a wavefront (lanes that differ in the bits above LPK),
+// left in every lane: DPP row rotation by 8 (slots of 8 lanes), then gfx950's row swaps
+// (v_permlane16_swap pairs rows 0-1 and 2-3, v_permlane32_swap the two halves), all VALU.
+template <uint32_t LPK, bool MAX>
+__device__ __forceinline__ float slots_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if (LPK <= 8) v = op(v, dpp_mov<0x128>(v));  // row_ror:8 = lane xor 8 within a row
+  if (LPK <= 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+template <uint32_t HD, int G, bool ADJ>
+__global__ __launch_bounds__(256) void k_attn_dec2(AttnDecK a) {
+  constexpr uint32_t LPK = HD / 8, KPW = 64 / LPK, NW = AD_WAVES;
   __shared__ float wm[AD_WAVES][G], wl[AD_WAVES][G];
   __shared__ float wo[AD_WAVES][G][HD];
   const uint32_t lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t kv = blockIdx.x, z = blockIdx.y, g = a.group;
-  auto el = [&](int e) -> uint32_t { return ADJ ? EL * lane + e : lane + 64 * e; };
+  const uint32_t slot = lane / LPK, sub = lane % LPK;
+  const uint32_t e0 = 4 * sub, e1 = HD / 2 + 4 * sub;  // this lane's two 4-element pieces
   // ---- loads that do not depend on the position
-  float q[G][EL], kn[EL], vn[EL], qw[EL], kw[EL];
+  float4 q[G][2], kn[2], vn[2], qw[2], kw[2];
 #pragma unroll
-  for (int i = 0; i < G; i++)
-#pragma unroll
-    for (int e = 0; e < EL; e++) q[i][e] = (uint32_t)i < g ? a.q[((uint64_t)kv * g + i) * HD + el(e)] : 0.f;
-#pragma unroll
-  for (int e = 0; e < EL; e++) {
-    kn[e] = a.k[(uint64_t)kv * HD + el(e)];
-    vn[e] = a.v[(uint64_t)kv * HD + el(e)];
-    qw[e] = a.mode == 0 ? a.qn[el(e)] : 1.f;
-    kw[e] = a.mode == 0 ? a.kn[el(e)] : 1.f;
+  for (int i = 0; i < G; i++) {
+    const float *qs = a.q + ((uint64_t)kv * g + ((uint32_t)i < g ? i : 0)) * HD;
+    q[i][0] = *(const float4 *)(qs + e0);
+    q[i][1] = *(const float4 *)(qs + e1);
   }
-  float cr[NP], sr[NP];
+  kn[0] = *(const float4 *)(a.k + (uint64_t)kv * HD + e0);
+  kn[1] = *(const float4 *)(a.k + (uint64_t)kv * HD + e1);
+  vn[0] = *(const float4 *)(a.v + (uint64_t)kv * HD + e0);
+  vn[1] = *(const float4 *)(a.v + (uint64_t)kv * HD + e1);
+  if (a.mode == 0) {
+    qw[0] = *(const float4 *)(a.qn + e0); qw[1] = *(const float4 *)(a.qn + e1);
+    kw[0] = *(const float4 *)(a.kn + e0); kw[1] = *(const float4 *)(a.kn + e1);
+  }
+  // rotation of this lane's pairs: adjacent pairs (e, e+1) inside a piece, or half-split
+  // pairs (e0 + c, e1 + c) across the two pieces
+  float cr[4], sr[4];
+  const uint32_t half = a.rot / 2;
+  if (ADJ) {
 #pragma unroll
-  for (int e = 0; e < (int)NP; e++) {
-    const uint32_t pi = ADJ ? NP * lane + e : lane + 64 * e;
-    cr[e] = a.cs[pi];
-    sr[e] = a.cs[a.rot / 2 + pi];
+    for (int c = 0; c < 4; c++) {
+      const uint32_t pi = (c < 2 ? e0 : e1) / 2 + (c & 1);
+      cr[c] = a.cs[pi]; sr[c] = a.cs[half + pi];
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; c++) { cr[c] = a.cs[e0 + c]; sr[c] = a.cs[half + e0 + c]; }
   }
   const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane(*a.pos);
   const uint32_t end = pos + 1, win = end < a.window ? end : a.window, begin = end - win;
   const uint32_t lo = begin + z * a.chunk;
   if (lo >= end) return;
   const uint32_t hi = lo + a.chunk < end ? lo + a.chunk : end;
-  const uint32_t nb = a.chunk / (AD_WAVES * AD_KPB);
   const uint64_t rowf = (uint64_t)a.kvh * HD;
-  float kr[AD_KPB][EL], vr[AD_KPB][EL];
+  // ---- the first batch of keys goes out before the norm and rotation arithmetic
+  float4 kb[AD2_DB][2], vb[AD2_DB][2];
+  auto key_of = [&](uint32_t b, uint32_t d) { return lo + ((b * AD2_DB + d) * NW + w) * KPW + slot; };
   auto load_batch = [&](uint32_t b) {
 #pragma unroll
-    for (uint32_t k = 0; k < AD_KPB; k++) {
-      uint32_t t = lo + (b * AD_WAVES + w) * AD_KPB + k;
-      if (t >= hi) t = lo;
-      const uint64_t base = (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD;
-#pragma unroll
-      for (int e = 0; e < EL; e++) { kr[k][e] = a.kc[base + el(e)]; vr[k][e] = a.vc[base + el(e)]; }
+    for (uint32_t d = 0; d < AD2_DB; d++) {
+      uint32_t t = key_of(b, d);
+      if (t >= hi) t = lo;  // masked below; any valid row
+      const float *kr = a.kc + (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD, *vr = a.vc + (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD;
+      kb[d][0] = *(const float4 *)(kr + e0); kb[d][1] = *(const float4 *)(kr + e1);
+      vb[d][0] = *(const float4 *)(vr + e0); vb[d][1] = *(const float4 *)(vr + e1);
     }
   };
   load_batch(0);
-  // ---- Q/K norm and rotation in registers
+  // ---- Q/K RMSNorm (mode 0) and rotation, in registers
+  auto sq4 = [](const float4 &v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; };
+  auto mul4 = [](const float4 &v, const float4 &u, float f) { return make_float4(v.x * u.x * f, v.y * u.y * f, v.z * u.z * f, v.w * u.w * f); };
   if (a.mode == 0) {
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < EL; e++) ss += q[i][e] * q[i][e];
-      const float inv = 1.f / sqrtf(wave_total(ss) / (float)HD + a.eps);
-#pragma unroll
-      for (int e = 0; e < EL; e++) q[i][e] = q[i][e] * qw[e] * inv;
+      const float inv = 1.f / sqrtf(group_sum<LPK>(sq4(q[i][0]) + sq4(q[i][1])) / (float)HD + a.eps);
+      q[i][0] = mul4(q[i][0], qw[0], inv); q[i][1] = mul4(q[i][1], qw[1], inv);
     }
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < EL; e++) ss += kn[e] * kn[e];
-    const float inv = 1.f / sqrtf(wave_total(ss) / (float)HD + a.eps);
-#pragma unroll
-    for (int e = 0; e < EL; e++) kn[e] = kn[e] * kw[e] * inv;
+    const float inv = 1.f / sqrtf(group_sum<LPK>(sq4(kn[0]) + sq4(kn[1])) / (float)HD + a.eps);
+    kn[0] = mul4(kn[0], kw[0], inv); kn[1] = mul4(kn[1], kw[1], inv);
   }
+  auto rot = [&](float4 (&v)[2]) {
+    if (ADJ) {
+      // pairs (x, y) and (z, w) of each piece: rotation slots 0, 1 (piece 0) and 2, 3 (piece 1)
+      float x, y;
+      x = v[0].x; y = v[0].y; v[0].x = x * cr[0] - y * sr[0]; v[0].y = x * sr[0] + y * cr[0];
+      x = v[0].z; y = v[0].w; v[0].z = x * cr[1] - y * sr[1]; v[0].w = x * sr[1] + y * cr[1];
+      x = v[1].x; y = v[1].y; v[1].x = x * cr[2] - y * sr[2]; v[1].y = x * sr[2] + y * cr[2];
+      x = v[1].z; y = v[1].w; v[1].z = x * cr[3] - y * sr[3]; v[1].w = x * sr[3] + y * cr[3];
+    } else {
+      float *p0 = &v[0].x, *p1 = &v[1].x;
 #pragma unroll
-  for (int e = 0; e < (int)NP; e++) {
-    const float c = cr[e], sn = sr[e];
-    const int ia = ADJ ? 2 * e : e, ib = ADJ ? 2 * e + 1 : e + (int)NP;
-#pragma unroll
-    for (int i = 0; i < G; i++) {
-      const float xa = q[i][ia], xb = q[i][ib];
-      q[i][ia] = xa * c - xb * sn;
-      q[i][ib] = xa * sn + xb * c;
+      for (int c = 0; c < 4; c++) {
+        const float xa = p0[c], xb = p1[c];
+        p0[c] = xa * cr[c] - xb * sr[c];
+        p1[c] = xa * sr[c] + xb * cr[c];
+      }
     }
-    const float xa = kn[ia], xb = kn[ib];
-    kn[ia] = xa * c - xb * sn;
-    kn[ib] = xa * sn + xb * c;
-  }
-  if (pos >= lo && pos < hi && w == 0) {
-    const uint64_t slot = (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
+  };
 #pragma unroll
-    for (int e = 0; e < EL; e++) { a.kc[slot + el(e)] = kn[e]; a.vc[slot + el(e)] = vn[e]; }
+  for (int i = 0; i < G; i++) rot(q[i]);
+  rot(kn);
+  if (pos >= lo && pos < hi && w == 0 && slot == 0) {
+    float *ks = a.kc + (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD, *vs = a.vc + (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
+    *(float4 *)(ks + e0) = kn[0]; *(float4 *)(ks + e1) = kn[1];
+    *(float4 *)(vs + e0) = vn[0]; *(float4 *)(vs + e1) = vn[1];
   }
   // ---- keys
-  float m[G], l[G], o[G][EL];
+  float m[G], l[G];
+  float4 o[G][2];
 #pragma unroll
-  for (int i = 0; i < G; i++) {
-    m[i] = -INFINITY; l[i] = 0.f;
-#pragma unroll
-    for (int e = 0; e < EL; e++) o[i][e] = 0.f;
-  }
+  for (int i = 0; i < G; i++) { m[i] = -INFINITY; l[i] = 0.f; o[i][0] = o[i][1] = make_float4(0.f, 0.f, 0.f, 0.f); }
+  const uint32_t nb = (a.chunk + AD2_DB * NW * KPW - 1) / (AD2_DB * NW * KPW);
+  auto dot8 = [](const float4 (&x)[2], const float4 (&y)[2]) {
+    float s = x[0].x * y[0].x;
+    s = fmaf(x[0].y, y[0].y, s); s = fmaf(x[0].z, y[0].z, s); s = fmaf(x[0].w, y[0].w, s);
+    s = fmaf(x[1].x, y[1].x, s); s = fmaf(x[1].y, y[1].y, s); s = fmaf(x[1].z, y[1].z, s);
+    return fmaf(x[1].w, y[1].w, s);
+  };
   for (uint32_t b = 0; b < nb; b++) {
+    if (lo + (b * AD2_DB * NW + w) * KPW >= hi) break;  // uniform: this wavefront's keys are all past the chunk
     if (b > 0) load_batch(b);
-    const uint32_t t0 = lo + (b * AD_WAVES + w) * AD_KPB;
-    if (t0 >= hi) break;  // uniform: later batches of this wavefront are past the chunk too
-    float sc[AD_KPB][G];
+    float sc[AD2_DB][G];
 #pragma unroll
-    for (uint32_t k = 0; k < AD_KPB; k++) {
-      if (t0 + k == pos) {
-#pragma unroll
-        for (int e = 0; e < EL; e++) { kr[k][e] = kn[e]; vr[k][e] = vn[e]; }
-      }
+    for (uint32_t d = 0; d < AD2_DB; d++) {
+      const uint32_t t = key_of(b, d);
+      if (t == pos) { kb[d][0] = kn[0]; kb[d][1] = kn[1]; vb[d][0] = vn[0]; vb[d][1] = vn[1]; }
 #pragma unroll
       for (int i = 0; i < G; i++) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < EL; e++) d += q[i][e] * kr[k][e];
-        sc[k][i] = t0 + k < hi ? wave_total(d) * a.scale : -INFINITY;
+        const float s = group_sum<LPK>(dot8(q[i], kb[d])) * a.scale;
+        sc[d][i] = t < hi ? s : -INFINITY;
       }
     }
 #pragma unroll
     for (int i = 0; i < G; i++) {
       float bm = sc[0][i];
 #pragma unroll
-      for (uint32_t k = 1; k < AD_KPB; k++) bm = fmaxf(bm, sc[k][i]);
-      const float mn = fmaxf(m[i], bm);  // finite: key t0 is inside the chunk
+      for (uint32_t d = 1; d < AD2_DB; d++) bm = fmaxf(bm, sc[d][i]);
+      const float mn = fmaxf(m[i], bm);
       const float corr = m[i] == -INFINITY ? 0.f : expf(m[i] - mn);
       float ps = 0.f;
+      float4 o0 = make_float4(o[i][0].x * corr, o[i][0].y * corr, o[i][0].z * corr, o[i][0].w * corr);
+      float4 o1 = make_float4(o[i][1].x * corr, o[i][1].y * corr, o[i][1].z * corr, o[i][1].w * corr);
 #pragma unroll
-      for (int e = 0; e < EL; e++) o[i][e] *= corr;
-#pragma unroll
-      for (uint32_t k = 0; k < AD_KPB; k++) {
-        const float p = sc[k][i] == -INFINITY ? 0.f : expf(sc[k][i] - mn);
+      for (uint32_t d = 0; d < AD2_DB; d++) {
+        const float p = sc[d][i] == -INFINITY ? 0.f : expf(sc[d][i] - mn);
         ps += p;
-#pragma unroll
-        for (int e = 0; e < EL; e++) o[i][e] += p * vr[k][e];
+        o0.x = fmaf(p, vb[d][0].x, o0.x); o0.y = fmaf(p, vb[d][0].y, o0.y); o0.z = fmaf(p, vb[d][0].z, o0.z); o0.w = fmaf(p, vb[d][0].w, o0.w);
+        o1.x = fmaf(p, vb[d][1].x, o1.x); o1.y = fmaf(p, vb[d][1].y, o1.y); o1.z = fmaf(p, vb[d][1].z, o1.z); o1.w = fmaf(p, vb[d][1].w, o1.w);
       }
+      o[i][0] = o0; o[i][1] = o1;
       l[i] = l[i] * corr + ps;
       m[i] = mn;
     }
   }
-  // ---- merge the wavefronts, then the chunks
+  // ---- merge the wavefront's key slots (lanes slot * LPK + sub), then the wavefronts
 #pragma unroll
   for (int i = 0; i < G; i++) {
-    if (lane == 0) { wm[w][i] = m[i]; wl[w][i] = l[i]; }
+    const float M = slots_reduce<LPK, true>(m[i]);
+    const float f = m[i] == -INFINITY ? 0.f : expf(m[i] - M);
+    const float L = slots_reduce<LPK, false>(l[i] * f);
+    float v8[8] = {o[i][0].x * f, o[i][0].y * f, o[i][0].z * f, o[i][0].w * f, o[i][1].x * f, o[i][1].y * f, o[i][1].z * f, o[i][1].w * f};
 #pragma unroll
-    for (int e = 0; e < EL; e++) wo[w][i][el(e)] = o[i][e];
+    for (int c = 0; c < 8; c++) v8[c] = slots_reduce<LPK, false>(v8[c]);
+    if (lane == 0) { wm[w][i] = M; wl[w][i] = L; }
+    if (slot == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) { wo[w][i][e0 + c] = v8[c]; wo[w][i][e1 + c] = v8[4 + c]; }
+    }
   }
   __syncthreads();
-  chunk_epilogue<G, HD>(a, kv, z, wm, wl, wo);
+  // the wavefronts' rescaling factors once per head, then the chunk's partial
+  __shared__ float wf[AD_WAVES][G], hM[G], hL[G];
+  if (threadIdx.x < (uint32_t)G) {
+    const uint32_t i = threadIdx.x;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) M = fmaxf(M, wm[u][i]);
+    float L = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) {
+      const float f = wm[u][i] == -INFINITY ? 0.f : expf(wm[u][i] - M);
+      wf[u][i] = f;
+      L += wl[u][i] * f;
+    }
+    hM[i] = M; hL[i] = L;
+  }
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < g * HD; j += blockDim.x) {
+    const uint32_t i = j / HD, d = j % HD;
+    float O = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < AD_WAVES; u++) O = fmaf(wo[u][i][d], wf[u][i], O);
+    float *pp = a.part + (((uint64_t)kv * g + i) * a.nsplit + z) * (HD + 2);
+    if (d == 0) { pp[0] = hM[i]; pp[1] = hL[i]; }
+    pp[2 + d] = O;
+  }
 }
 
 // Merge of the chunks of one query head: thread d owns output element d. The partials were
@@ -830,6 +911,7 @@ hipError_t rope_inv_freq(hipStream_t s, double *f, uint32_t rot, float theta) {
   return hipGetLastError();
 }
 
+static uint32_t dec2_chunk(uint32_t capacity, uint32_t kvh, uint32_t hd);
 static uint32_t dec_chunk(uint32_t capacity, uint32_t kvh) {
   // enough workgroups to cover the chip twice at full context, at most 512 keys each
   uint32_t nb = capacity * kvh / (AD_WAVES * AD_KPB * 2 * (uint32_t)device_cu_count());
@@ -842,31 +924,39 @@ bool decode_attention_supported(uint32_t heads, uint32_t kv_heads, uint32_t hd) 
   return (hd == 64 || hd == 128 || hd == 256) && kv_heads && heads % kv_heads == 0 && heads / kv_heads <= 8;
 }
 
+// Partials of either decode kernel (the full-rotation one chunks by dec2_chunk, the other
+// by dec_chunk).
 uint64_t decode_attention_scratch_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t capacity) {
-  const uint32_t chunk = dec_chunk(capacity, kv_heads);
-  return (uint64_t)heads * ((capacity + chunk - 1) / chunk) * (hd + 2);
+  const uint32_t c1 = dec_chunk(capacity, kv_heads), c2 = dec2_chunk(capacity, kv_heads, hd);
+  const uint32_t n1 = (capacity + c1 - 1) / c1, n2 = (capacity + c2 - 1) / c2;
+  return (uint64_t)heads * (n1 > n2 ? n1 : n2) * (hd + 2);
+}
+
+// Keys per workgroup of k_attn_dec2: whole load batches (AD2_DB * 4 wavefronts * KPW keys),
+// enough workgroups to cover the chip twice over the ring, at most AD_MAX_SPLITS chunks.
+static uint32_t dec2_chunk(uint32_t capacity, uint32_t kvh, uint32_t hd) {
+  const uint32_t batch = AD2_DB * AD_WAVES * (64 / (hd / 8));
+  uint32_t c = (uint32_t)(((uint64_t)capacity * kvh + 2 * device_cu_count() - 1) / (2 * device_cu_count()));
+  c = (c + batch - 1) / batch * batch;
+  if (c < batch) c = batch;
+  while ((capacity + c - 1) / c > AD_MAX_SPLITS) c += batch;
+  return c;
 }
 
 template <int EL>
 static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
-  // registers only: full-width rotation (rot == hd) with its pairs inside a lane (EL >= 2)
-  const bool fast = EL >= 2 && k.rot == 64u * EL;
-  if (fast) {
-    constexpr int E = EL >= 2 ? EL : 2;
-    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, k); };
-    if (k.mode == 2) {
-      if (k.group <= 1) go(k_attn_fast<E, 1, true>); else if (k.group <= 2) go(k_attn_fast<E, 2, true>);
-      else if (k.group <= 4) go(k_attn_fast<E, 4, true>); else go(k_attn_fast<E, 8, true>);
-    } else {
-      if (k.group <= 1) go(k_attn_fast<E, 1, false>); else if (k.group <= 2) go(k_attn_fast<E, 2, false>);
-      else if (k.group <= 4) go(k_attn_fast<E, 4, false>); else go(k_attn_fast<E, 8, false>);
-    }
-    return;
-  }
   if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec<EL, 1>), grid, dim3(256), 0, s, k);
   else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec<EL, 2>), grid, dim3(256), 0, s, k);
   else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec<EL, 4>), grid, dim3(256), 0, s, k);
   else hipLaunchKernelGGL((k_attn_dec<EL, 8>), grid, dim3(256), 0, s, k);
+}
+
+template <uint32_t HD, bool ADJ>
+static void launch_dec2(hipStream_t s, const AttnDecK &k, dim3 grid) {
+  if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec2<HD, 1, ADJ>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec2<HD, 2, ADJ>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec2<HD, 4, ADJ>), grid, dim3(256), 0, s, k);
+  else hipLaunchKernelGGL((k_attn_dec2<HD, 8, ADJ>), grid, dim3(256), 0, s, k);
 }
 
 hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
@@ -878,13 +968,20 @@ hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
   k.part = in.partial; k.pos = in.pos; k.cs = in.rope;
   k.heads = in.heads; k.kvh = in.kv_heads; k.rot = in.rot ? in.rot : in.hd; k.cap = in.capacity;
   k.window = in.window; k.group = in.heads / in.kv_heads;
-  k.chunk = dec_chunk(in.capacity, in.kv_heads);
+  // full-width rotation runs the 16-byte-lane kernel, partial rotation the generic one
+  const bool full = k.rot == in.hd;
+  k.chunk = full ? dec2_chunk(in.capacity, in.kv_heads, in.hd) : dec_chunk(in.capacity, in.kv_heads);
   const uint32_t keys = in.window < in.capacity ? in.window : in.capacity;
   k.nsplit = (keys + k.chunk - 1) / k.chunk;
   if (k.nsplit > AD_MAX_SPLITS) return hipErrorInvalidValue;
   k.scale = in.scale; k.eps = in.eps; k.mode = in.mode;
   const dim3 grid(in.kv_heads, k.nsplit);
-  if (in.hd == 64) launch_dec<1>(s, k, grid);
+  if (full) {
+    const bool adj = in.mode == 2;
+    if (in.hd == 64) adj ? launch_dec2<64, true>(s, k, grid) : launch_dec2<64, false>(s, k, grid);
+    else if (in.hd == 128) adj ? launch_dec2<128, true>(s, k, grid) : launch_dec2<128, false>(s, k, grid);
+    else adj ? launch_dec2<256, true>(s, k, grid) : launch_dec2<256, false>(s, k, grid);
+  } else if (in.hd == 64) launch_dec<1>(s, k, grid);
   else if (in.hd == 128) launch_dec<2>(s, k, grid);
   else launch_dec<4>(s, k, grid);
   WGD_HIP(hipGetLastError());
