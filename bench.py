@@ -223,6 +223,18 @@ def gemm_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, batch
             "tflops": flops / t / 1e12, "mfma_tflops": 3 * flops / t / 1e12, "mfma_frac": 3 * flops / t / PEAK_BF16}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), as the baseline's hardware."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(f: np.ndarray, title: str, seconds: float = 15.0) -> dict:
     from oracle import orc
     from webgpu_amd.context import attention_memory
@@ -238,9 +250,11 @@ def cpu_baseline(f: np.ndarray, title: str, seconds: float = 15.0) -> dict:
         tok, pos, n = int(np.argmax(logits)), pos + 1, n + 1
     dt = time.perf_counter() - t0
     m.close()
-    return {"value": n / dt, "unit": "tok/s", "cores": orc.threads(), "kind": "port",
+    cpu = cpu_model()
+    return {"value": n / dt, "unit": "tok/s", "cores": orc.threads(), "kind": "port", "cpu": cpu,
+            "host_cpus": os.cpu_count(),
             "sample": f"float64 C oracle, {title} decode: 8-token prompt then {n} greedy tokens "
-                      f"in {dt:.1f} s on {orc.threads()} threads ({platform.processor() or platform.machine()})"}
+                      f"in {dt:.1f} s on {orc.threads()} threads of {cpu}"}
 
 
 def main() -> None:

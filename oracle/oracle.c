@@ -311,6 +311,8 @@ static double gelu_tanh(double g) { return 0.5 * g * (1.0 + tanh(0.7978845608 * 
  * weights, engine.ts:138-180/217-251 and the Gemma-3 body :158-174). */
 int orc_model_forward(orc_model *m, const int32_t *ids, int32_t n, int32_t start, double *logits) {
   const orc_config *c = &m->c;
+  for (int b = 0; b < n; b++)
+    if (ids[b] < 0 || ids[b] >= m->embd.ne1) return 1;
   int64_t H = c->hidden, hd = c->head_dim, qd = (int64_t)c->heads * hd, kd = (int64_t)c->kv_heads * hd, F = c->intermediate;
   double *x = (double *)calloc((size_t)(n * H), sizeof(double));
   double *normed = (double *)malloc(sizeof(double) * n * H), *tmp = (double *)malloc(sizeof(double) * n * H);
@@ -319,7 +321,6 @@ int orc_model_forward(orc_model *m, const int32_t *ids, int32_t n, int32_t start
   double *gate = (double *)malloc(sizeof(double) * n * F), *up = (double *)malloc(sizeof(double) * n * F);
   int64_t eb = row_bytes(m->embd.type, H);
   for (int b = 0; b < n; b++) {
-    if (ids[b] < 0 || ids[b] >= m->embd.ne1) return 1;
     orc_dequant_row(m->embd.data + (int64_t)ids[b] * eb, m->embd.type, H, x + b * H);
     for (int64_t i = 0; i < H; i++) x[b * H + i] *= c->embed_scale;
   }

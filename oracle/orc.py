@@ -181,30 +181,36 @@ class OrcConfig(C.Structure):
         "epsilon", "theta", "local_theta", "attention_scale", "rope_scale", "embed_scale")]
 
 
+def config_struct(gguf, cfg, context: int) -> OrcConfig:
+    """The oracle's orc_config for a parsed GGUF and its model config."""
+    c = OrcConfig()
+    gemma = cfg.family == "gemma3"
+    c.family = 1 if gemma else 0
+    c.rope_adjacent = 1 if cfg.rope == "norm" else 0
+    c.hidden, c.intermediate, c.layers = cfg.hidden, cfg.intermediate, cfg.layers
+    c.heads, c.kv_heads, c.head_dim, c.vocab = cfg.heads, cfg.kvHeads, cfg.headDim, cfg.vocab
+    c.rotary_dim = cfg.rotaryDim
+    c.window = cfg.window if gemma else cfg.slidingWindow
+    c.period = cfg.period
+    c.qk_norm = int(cfg.qkNorm)
+    c.ffn_gate = int(cfg.ffnGate)
+    c.gelu = int(cfg.activation == "gelu")
+    c.bias_q, c.bias_k, c.bias_v, c.bias_output = (int(cfg.bias[k]) for k in ("q", "k", "v", "output"))
+    c.tied_output = 0 if "output.weight" in gguf.tensors else 1
+    c.context, c.batch = context, 128
+    c.epsilon, c.theta, c.local_theta = cfg.epsilon, cfg.theta, cfg.localTheta
+    c.attention_scale, c.rope_scale = cfg.attentionScale, cfg.ropeScale
+    c.embed_scale = math.sqrt(cfg.hidden) if cfg.architecture == "gemma3" else 1.0
+    return c
+
+
 class OracleModel:
     """The f64 reference forward over the raw bytes of a GGUF file."""
 
     def __init__(self, file: np.ndarray, gguf, cfg, context: int, capacities: Sequence[int]) -> None:
         self.file = np.ascontiguousarray(file, np.uint8)
         self.cfg = cfg
-        c = OrcConfig()
-        gemma = cfg.family == "gemma3"
-        c.family = 1 if gemma else 0
-        c.rope_adjacent = 1 if cfg.rope == "norm" else 0
-        c.hidden, c.intermediate, c.layers = cfg.hidden, cfg.intermediate, cfg.layers
-        c.heads, c.kv_heads, c.head_dim, c.vocab = cfg.heads, cfg.kvHeads, cfg.headDim, cfg.vocab
-        c.rotary_dim = cfg.rotaryDim
-        c.window = cfg.window if gemma else cfg.slidingWindow
-        c.period = cfg.period
-        c.qk_norm = int(cfg.qkNorm)
-        c.ffn_gate = int(cfg.ffnGate)
-        c.gelu = int(cfg.activation == "gelu")
-        c.bias_q, c.bias_k, c.bias_v, c.bias_output = (int(cfg.bias[k]) for k in ("q", "k", "v", "output"))
-        c.tied_output = 0 if "output.weight" in gguf.tensors else 1
-        c.context, c.batch = context, 128
-        c.epsilon, c.theta, c.local_theta = cfg.epsilon, cfg.theta, cfg.localTheta
-        c.attention_scale, c.rope_scale = cfg.attentionScale, cfg.ropeScale
-        c.embed_scale = math.sqrt(cfg.hidden) if cfg.architecture == "gemma3" else 1.0
+        c = config_struct(gguf, cfg, context)
         caps = (C.c_int32 * cfg.layers)(*capacities)
         self.m = lib().orc_model_create(C.byref(c), caps)
         base = self.file.ctypes.data

@@ -37,8 +37,8 @@ def build(name, context, batch=128):
     return f, g, c, caps, eng
 
 
-def check_model(name, prompt_len, steps, context=512, chunk=128, seed=7):
-    f, g, c, caps, eng = build(name, context)
+def check_model(name, prompt_len, steps, context=512, chunk=128, seed=7, batch=128):
+    f, g, c, caps, eng = build(name, context, batch)
     try:
         ora = orc.OracleModel(f, g, c, context, caps)
         ids = synth.prompt_ids(c.vocab, prompt_len, seed)
@@ -81,6 +81,14 @@ def test_tiny_check_dense_tokens_and_logits():
         assert eng.tokensInCache == ids + toks[:3]
     finally:
         eng.dispose()
+
+
+@pytest.mark.parametrize("name,prompt,steps", [("mini-gemma3", 40, 8), ("mini-llama", 20, 8)])
+def test_mini_models_tokens_and_logits(name, prompt, steps):
+    """Gemma-3 local rings of 23 slots wrapped by a 40-token prompt in 8-token batches at
+    head_dim 64; Q8_0 projections and adjacent-pair rotation at head_dim 32."""
+    eng, *_ = check_model(name, prompt, steps, context=256, chunk=8, seed=8, batch=8)
+    eng.dispose()
 
 
 def test_tiny_device_decode_matches_eager_steps():

@@ -1,0 +1,63 @@
+"""libwgd's host code under AddressSanitizer + UndefinedBehaviorSanitizer, on the GPU.
+
+tests/native/wgd_san links the library's sources compiled with the host pass sanitized
+(-Xarch_host -fsanitize=address,undefined; device code is built as usual) to a driver of
+the C ABI. A heap overflow, use after free, leak or undefined operation in argument checks,
+launch planning, buffer and model bookkeeping or graph capture ends the run with a report.
+The model runs must give the uninstrumented library's logits and tokens bit for bit.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from tests.native.bundle import write_bundle
+from webgpu_amd.engine import LoadOptions, PagedEngine
+
+pytestmark = pytest.mark.gpu
+NATIVE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native")
+EXE = os.path.join(NATIVE, "_build", "wgd_san")
+ENV = dict(os.environ,
+           ASAN_OPTIONS="detect_leaks=1:halt_on_error=1:protect_shadow_gap=0",
+           LSAN_OPTIONS="suppressions=" + os.path.join(NATIVE, "lsan.supp"),
+           UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+
+
+def run(args):
+    assert os.path.exists(EXE), "tests/native/_build/wgd_san is not built (make -C tests/native wgd)"
+    print(f"\nwgd_san {' '.join(args[1:2])}", flush=True)
+    r = subprocess.run(args, capture_output=True, text=True, env=ENV, timeout=300)
+    report = r.stdout + r.stderr
+    assert r.returncode == 0 and "Sanitizer" not in report and "runtime error" not in report, report[-6000:]
+    return report
+
+
+def test_c_abi_under_host_sanitizers():
+    assert "ok" in run([EXE, "api"])
+
+
+@pytest.mark.parametrize("name,prompt,chunk,steps", [("tiny", 12, 8, 4), ("mini-gemma3", 40, 8, 6),
+                                                     ("mini-llama", 20, 8, 5)])
+def test_model_under_host_sanitizers(tmp_path, name, prompt, chunk, steps):
+    path, out = str(tmp_path / "m.bundle"), str(tmp_path / "m.out")
+    f, g, c, caps, ids = write_bundle(path, name, 256, chunk, prompt, steps)
+    run([EXE, "model", path, out])
+    raw = np.fromfile(out, np.uint8)
+    v = c.vocab
+    first = raw[:4 * v].view(np.float32)
+    toks = raw[4 * v:4 * v + 4 * steps].view(np.int32).tolist()
+    last = raw[4 * v + 4 * steps:].view(np.float32)
+    eng = PagedEngine()
+    eng.load(f, LoadOptions(contextLength=256, batchSize=chunk))
+    try:
+        for i in range(0, prompt, chunk):
+            got = eng.forward(ids[i:i + chunk], i, i + chunk >= prompt)
+        np.testing.assert_array_equal(first, got)
+        want = [int(np.argmax(got))] + eng.decode(int(np.argmax(got)), prompt, steps - 2)
+        lg = eng.forward([want[-1]], prompt + steps - 2, True)
+        want.append(int(np.argmax(lg)))
+        assert toks == want
+        np.testing.assert_array_equal(last, lg)
+    finally:
+        eng.dispose()

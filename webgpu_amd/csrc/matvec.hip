@@ -725,25 +725,18 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
   MVPlan best_p{};
   const uint32_t N = chunk_elems(w.type), C = w.cols / N, CQ = (C + 7) / 8;
   const uint32_t cus = (uint32_t)device_cu_count();
-  static const int env_ns = getenv("WGD_MV_NS") ? atoi(getenv("WGD_MV_NS")) : 0;
-  static const int env_iter = getenv("WGD_MV_ITER") ? atoi(getenv("WGD_MV_ITER")) : 0;
-  static const int env_nr = getenv("WGD_MV_NR") ? atoi(getenv("WGD_MV_NR")) : 0;
-  static const int env_du = getenv("WGD_MV_DU") ? atoi(getenv("WGD_MV_DU")) : 0;
   const uint32_t dumax = glu ? 2 : 4;
   // unique weight bytes of one unit (16 rows x 8 chunk columns and its scale planes), KB
   const double unit_kb = w.type == Q6_K ? 2.625 : w.type == Q5_K ? 2.75 : w.type == Q8_0 ? 2.125 : 2.25;
   double best_cost = 1e30;
   for (uint32_t ns = 1; ns <= 16; ns++) {
-    if (env_ns && (int)ns != env_ns) continue;
     const uint32_t nsb = (CQ + ns - 1) / ns;
     if ((nsb - 1) * ns >= CQ && ns > 1) continue;  // a slice would be empty
     const uint32_t waste = ns * nsb * 8 - C;
     if (waste * 7 > C && ns > 1) continue;
     const uint32_t ke = ns * nsb * 8 * N;
     for (uint32_t nr = 1; nr * ns <= 16; nr++) {
-      if (env_nr && (int)nr != env_nr) continue;
       for (uint32_t iter = 1; iter <= 256; iter++) {
-        if (env_iter && (int)iter != env_iter) continue;
         const uint32_t rt = 16 * nr * iter;
         if (rt > 64 * nr * ns || rt > 1024) break;  // one epilogue thread per row
         if (quantized_out && rt % 16) continue;
@@ -762,7 +755,6 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
         // that keeps a CU's loads in flight within ~100 KB
         uint32_t du = dumax;
         while (du > 1 && (nsb % du || inflight(du) > 100.0)) du /= 2;
-        if (env_du) { if (nsb % (uint32_t)env_du || (uint32_t)env_du > dumax) continue; du = (uint32_t)env_du; }
         double cost = (double)rounds * rt * (1.0 + (double)waste / C);
         if (inflight(du) < 64.0) cost *= 64.0 / inflight(du);
         cost *= 1.0 + 2.0 / rt;  // activation staging per workgroup

@@ -67,7 +67,6 @@ struct wgd_model {
   uint64_t *arg_part = nullptr; uint32_t arg_entries = 0;  // head argmax keys (quantized path)
   float *att_part = nullptr; uint64_t att_part_floats = 0;
   GemmScratch gemm_part;          // split-K partial sums of the prompt GEMMs
-  bool use_graph = true;         // WGD_GRAPH=0 disables capture (profilers, debugging)
   // Quantized-activation decode path (every matrix Q4_K, Q6_K or Q8_0): activation buffers
   // in the QX format.
   bool qpath = false;
@@ -547,8 +546,6 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
   m->L.resize(c.layers);
   m->seen.assign(c.layers, 0);
   ctx->models.insert(m);
-  const char *g = getenv("WGD_GRAPH");
-  m->use_graph = !(g && g[0] == '0');
   const uint64_t B = c.batch, H = c.hidden, qd = (uint64_t)c.heads * c.head_dim, kd = (uint64_t)c.kv_heads * c.head_dim,
                  F = c.intermediate;
   int rc = WGD_OK;
@@ -766,8 +763,6 @@ int wgd_model_ready(wgd_model *m) {
         mv_supported(L.up) && mv_supported(L.down) &&
         (!c.ffn_gate || (mv_supported(L.gate) && L.gate.type == L.up.type && L.gate.layout == L.up.layout));
   }
-  const char *env = getenv("WGD_QMATVEC");
-  if (env && env[0] == '0') q = false;
   if (q) {
     const uint32_t H = c.hidden, qd = c.heads * c.head_dim, F = c.intermediate;
     rc = alloc(m, qx_bytes(H), "qx attn", &m->qx_attn);
@@ -783,8 +778,7 @@ int wgd_model_ready(wgd_model *m) {
       for (const Layer &L : m->L) if (!L.q_norm || !L.k_norm) return false;
       return true;
     }();
-    const char *fa = getenv("WGD_FUSED_ATTENTION");
-    m->fused_attention = decode_attention_supported(c.heads, c.kv_heads, c.head_dim) && norms && !(fa && fa[0] == '0');
+    m->fused_attention = decode_attention_supported(c.heads, c.kv_heads, c.head_dim) && norms;
     if (m->fused_attention) {
       // one table per distinct theta: the model's, and Gemma's local layers'
       const uint32_t rot = is_gemma(m) || !c.rotary_dim ? (uint32_t)c.head_dim : (uint32_t)c.rotary_dim;
@@ -862,11 +856,7 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count, 
   if (rc) return rc;
   hipGraph_t &graph = m->sampling ? m->graph_s : m->graph;
   hipGraphExec_t &exec = m->sampling ? m->exec_s : m->exec;
-  if (!m->use_graph) {
-    // Eager launches (WGD_GRAPH=0): same kernels, one host launch each; used under tracers.
-    for (int32_t i = 0; i < count && !rc; i++) rc = ctx_check(ctx, decode_step(m, true), "decode");
-    if (rc) return rc;
-  } else if (!exec) {
+  if (!exec) {
     // Run one step eagerly first: it validates every launch outside capture.
     rc = ctx_check(ctx, decode_step(m, true), "decode");
     if (!rc) rc = ctx_sync(ctx, "GPU fault during decode");

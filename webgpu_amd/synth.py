@@ -166,6 +166,15 @@ SPECS: Dict[str, Spec] = {
     "gemma3-27b-6l": Spec("gemma3-27b-6l", "gemma3", 6, 5376, 32, 16, 128, 21504, 262144, 1e-6, 1_000_000.0, True,
                           True, {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K},
                           context_length=131072),
+    # Small quantized models for the sanitizer runs: every weight type, both rope modes, a
+    # Gemma-3 layer period of six with 16-token local windows (a 40-token prompt in 8-token
+    # batches wraps their rings) and head dims off the 64/128/256 fast paths.
+    "mini-gemma3": Spec("mini-gemma3", "gemma3", 6, 256, 4, 2, 64, 512, 1024, 1e-6, 1_000_000.0, True, True,
+                        {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K}, window=16,
+                        context_length=4096, seed=21),
+    "mini-llama": Spec("mini-llama", "llama", 3, 256, 8, 2, 32, 768, 512, 1e-5, 500_000.0, False, False,
+                       {"embd": Q8_0, "output": Q6_K, "attn": Q8_0, "v": Q8_0, "ffn": Q4_K},
+                       context_length=4096, seed=22),
 }
 
 
