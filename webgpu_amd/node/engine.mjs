@@ -3,8 +3,9 @@
 // TokenEvents, forward, reset, dispose, info and the device token pick. GGUF parsing,
 // modelConfig and ring sizing run here as in gguf.ts / context.ts; weights are uploaded
 // once and stay resident (the weight pager collapses), and every forward and decode
-// step runs in libwgd on the GPU. The host keeps the reference's tokenizers: prompts are ids, or
-// any object with chat(messages) -> ids, decode(ids) -> string and eos passed as tokenizer.
+// step runs in libwgd on the GPU. The Node host has no tokenizer of its own: prompts are ids,
+// or any object with chat(messages) -> ids, decode(ids) -> string and eos passed as
+// `tokenizer`, which is where the reference's TypeScript tokenizers plug in.
 import { createRequire } from 'module';
 import { readGGUF, modelConfig, FileSource } from './gguf.mjs';
 import { attentionMemory, validateContext, outputLimit, MAX_CONTEXT } from './context.mjs';

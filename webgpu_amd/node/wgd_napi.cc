@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -16,8 +17,16 @@
 
 namespace {
 
+// The context lives in a shared record: the context handle, its models and its buffers each
+// hold a reference, so a wrapper collected late never points at freed host memory, and
+// destroy() (which frees the device side) leaves ctx NULL for every holder to see.
+// Every wrapper starts with a tag, so a handle of one kind passed where another is expected
+// is refused instead of being read as the wrong type.
 struct Ctx { wgd_context *ctx = nullptr; };
-struct Model { wgd_model *m = nullptr; Ctx *owner = nullptr; int32_t vocab = 0; };
+using CtxRef = std::shared_ptr<Ctx>;
+struct CtxHandle { static constexpr uint32_t TAG = 0x77676443; uint32_t tag = TAG; CtxRef c; };
+struct Model { static constexpr uint32_t TAG = 0x7767644d; uint32_t tag = TAG; wgd_model *m = nullptr; CtxRef owner; int32_t vocab = 0; };
+struct Buf { static constexpr uint32_t TAG = 0x77676442; uint32_t tag = TAG; wgd_buffer *b = nullptr; CtxRef owner; };
 
 napi_value undefined(napi_env env) {
   napi_value u;
@@ -52,9 +61,13 @@ napi_value throw_status(napi_env env, wgd_context *ctx, int st) {
 
 template <class T>
 T *unwrap(napi_env env, napi_value v) {
+  napi_valuetype vt;
   void *p = nullptr;
-  if (napi_get_value_external(env, v, &p) != napi_ok) return nullptr;
-  return (T *)p;
+  if (napi_typeof(env, v, &vt) != napi_ok || vt != napi_external) return nullptr;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return nullptr;
+  uint32_t tag;
+  std::memcpy(&tag, p, sizeof tag);
+  return tag == T::TAG ? (T *)p : nullptr;
 }
 
 bool get_i32(napi_env env, napi_value v, int32_t *out) { return napi_get_value_int32(env, v, out) == napi_ok; }
@@ -94,22 +107,24 @@ napi_value create(napi_env env, napi_callback_info info) {
   wgd_context *ctx = nullptr;
   int st = wgd_create(dev, budget, &ctx);
   if (st != WGD_OK) return throw_status(env, ctx, st);
-  Ctx *c = new Ctx{ctx};
-  return make_external(env, c, [](napi_env, void *p, void *) { delete (Ctx *)p; });
+  CtxHandle *h = new CtxHandle();
+  h->c = std::make_shared<Ctx>();
+  h->c->ctx = ctx;
+  return make_external(env, h, [](napi_env, void *p, void *) { delete (CtxHandle *)p; });
 }
 
 // destroy(context): frees every device allocation of the context (gpu.ts:66)
 napi_value destroy(napi_env env, napi_callback_info info) {
   ARGS(1);
-  Ctx *c = unwrap<Ctx>(env, argv[0]);
-  if (c && c->ctx) { wgd_destroy(c->ctx); c->ctx = nullptr; }
+  CtxHandle *h = unwrap<CtxHandle>(env, argv[0]);
+  if (h && h->c->ctx) { wgd_destroy(h->c->ctx); h->c->ctx = nullptr; }
   return undefined(env);
 }
 
 Ctx *live_ctx(napi_env env, napi_value v) {
-  Ctx *c = unwrap<Ctx>(env, v);
-  if (!c || !c->ctx) { throw_msg(env, "WGD_E_STATE", "The GPU context was disposed."); return nullptr; }
-  return c;
+  CtxHandle *h = unwrap<CtxHandle>(env, v);
+  if (!h || !h->c->ctx) { throw_msg(env, "WGD_E_STATE", "The GPU context was disposed."); return nullptr; }
+  return h->c.get();
 }
 
 napi_value adapter_name(napi_env env, napi_callback_info info) {
@@ -186,7 +201,10 @@ napi_value model_create(napi_env env, napi_callback_info info) {
     return throw_msg(env, "WGD_E_INVALID", "capacities must be an Int32Array with one entry per layer");
   wgd_model *m = nullptr;
   CHECK(c->ctx, wgd_model_create(c->ctx, &cfg, (const int32_t *)caps, &m));
-  Model *w = new Model{m, c, cfg.vocab};
+  Model *w = new Model();
+  w->m = m;
+  w->owner = unwrap<CtxHandle>(env, argv[0])->c;
+  w->vocab = cfg.vocab;
   return make_external(env, w, [](napi_env, void *p, void *) { delete (Model *)p; });
 }
 
@@ -301,12 +319,453 @@ napi_value model_destroy(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---------------------------------------------------------------- buffers and launchers
+// One function per C-ABI entry point of include/wgd.h, arguments in the same order, the
+// context first. Buffers are externals of the context that made them; sizes, offsets and
+// counts are non-negative integer Numbers (exact up to 2^53).
+
+bool get_u64(napi_env env, napi_value v, uint64_t *out) {
+  double d = 0;
+  if (!get_f64(env, v, &d) || !(d >= 0) || d > 9007199254740992.0 || d != (double)(uint64_t)d) return false;
+  *out = (uint64_t)d;
+  return true;
+}
+bool get_u32(napi_env env, napi_value v, uint32_t *out) {
+  uint64_t u = 0;
+  if (!get_u64(env, v, &u) || u > 0xFFFFFFFFull) return false;
+  *out = (uint32_t)u;
+  return true;
+}
+bool is_nullish(napi_env env, napi_value v) {
+  napi_valuetype vt;
+  napi_typeof(env, v, &vt);
+  return vt == napi_null || vt == napi_undefined;
+}
+
+// Any typed array: its data pointer and length in bytes.
+bool typed_bytes(napi_env env, napi_value v, void **data, uint64_t *bytes) {
+  bool is = false;
+  napi_is_typedarray(env, v, &is);
+  if (!is) return false;
+  napi_typedarray_type t;
+  size_t count = 0, off = 0;
+  napi_value ab;
+  if (napi_get_typedarray_info(env, v, &t, &count, data, &ab, &off) != napi_ok) return false;
+  size_t el = 1;
+  switch (t) {
+    case napi_int16_array: case napi_uint16_array: el = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: el = 8; break;
+    default: el = 1;
+  }
+  *bytes = (uint64_t)count * el;
+  return true;
+}
+
+// A buffer argument: a live buffer of context c (NULL allowed when `optional`). On false an
+// error is pending.
+bool buf_arg(napi_env env, napi_value v, const Ctx *c, wgd_buffer **out, bool optional) {
+  *out = nullptr;
+  if (optional && is_nullish(env, v)) return true;
+  Buf *b = unwrap<Buf>(env, v);
+  if (!b || !b->b || b->owner.get() != c) {
+    throw_msg(env, "WGD_E_INVALID", "expected a live buffer of this context");
+    return false;
+  }
+  *out = b->b;
+  return true;
+}
+
+#define CTX_ARG() \
+  Ctx *c = live_ctx(env, argv[0]); \
+  if (!c) return nullptr
+#define BUF_ARG(i, name) \
+  wgd_buffer *name = nullptr; \
+  if (!buf_arg(env, argv[i], c, &name, false)) return nullptr
+#define OPT_BUF_ARG(i, name) \
+  wgd_buffer *name = nullptr; \
+  if (!buf_arg(env, argv[i], c, &name, true)) return nullptr
+#define U32_ARG(i, name) \
+  uint32_t name = 0; \
+  if (!get_u32(env, argv[i], &name)) return throw_msg(env, "WGD_E_INVALID", #name " must be an integer in [0, 2^32)")
+#define U64_ARG(i, name) \
+  uint64_t name = 0; \
+  if (!get_u64(env, argv[i], &name)) return throw_msg(env, "WGD_E_INVALID", #name " must be an integer in [0, 2^53]")
+#define I32_ARG(i, name) \
+  int32_t name = 0; \
+  if (!get_i32(env, argv[i], &name)) return throw_msg(env, "WGD_E_INVALID", #name " must be a number")
+#define F64_ARG(i, name) \
+  double name = 0; \
+  if (!get_f64(env, argv[i], &name)) return throw_msg(env, "WGD_E_INVALID", #name " must be a number")
+
+napi_value wrap_buffer(napi_env env, const Ctx *c, napi_value ctx_value, wgd_buffer *b) {
+  Buf *w = new Buf();
+  w->b = b;
+  w->owner = unwrap<CtxHandle>(env, ctx_value)->c;
+  (void)c;
+  return make_external(env, w, [](napi_env, void *p, void *) { delete (Buf *)p; });
+}
+
+napi_value num(napi_env env, double d) {
+  napi_value r;
+  napi_create_double(env, d, &r);
+  return r;
+}
+
+// bufferCreate(ctx, size, label) -> buffer (Compute.buffer, gpu.ts:24-30)
+napi_value buffer_create(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  CTX_ARG();
+  U64_ARG(1, size);
+  std::string label = "buffer";
+  if (!is_nullish(env, argv[2])) {
+    size_t len = 0;
+    napi_get_value_string_utf8(env, argv[2], nullptr, 0, &len);
+    label.assign(len, '\0');
+    napi_get_value_string_utf8(env, argv[2], &label[0], len + 1, &len);
+  }
+  wgd_buffer *b = nullptr;
+  CHECK(c->ctx, wgd_buffer_create(c->ctx, size, label.c_str(), &b));
+  return wrap_buffer(env, c, argv[0], b);
+}
+
+// bufferDestroy(ctx, buffer) (Compute.destroy, gpu.ts:31)
+napi_value buffer_destroy(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  CTX_ARG();
+  Buf *w = unwrap<Buf>(env, argv[1]);
+  if (!w || !w->b || w->owner.get() != c) return throw_msg(env, "WGD_E_INVALID", "expected a live buffer of this context");
+  CHECK(c->ctx, wgd_buffer_destroy(c->ctx, w->b));
+  w->b = nullptr;
+  return undefined(env);
+}
+
+napi_value buffer_size(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  CTX_ARG();
+  BUF_ARG(1, b);
+  return num(env, (double)wgd_buffer_size(b));
+}
+
+// uploadWeights(ctx, type, cols, rows, data: Uint8Array, label) -> buffer
+napi_value upload_weights(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  CTX_ARG();
+  I32_ARG(1, type);
+  U32_ARG(2, cols);
+  U32_ARG(3, rows);
+  void *data = nullptr;
+  size_t bytes = 0;
+  if (!typed(env, argv[4], napi_uint8_array, &data, &bytes)) return throw_msg(env, "WGD_E_INVALID", "data must be a Uint8Array");
+  std::string label = "weights";
+  if (!is_nullish(env, argv[5])) {
+    size_t len = 0;
+    napi_get_value_string_utf8(env, argv[5], nullptr, 0, &len);
+    label.assign(len, '\0');
+    napi_get_value_string_utf8(env, argv[5], &label[0], len + 1, &len);
+  }
+  wgd_buffer *b = nullptr;
+  CHECK(c->ctx, wgd_upload_weights(c->ctx, type, cols, rows, data, bytes, label.c_str(), &b));
+  return wrap_buffer(env, c, argv[0], b);
+}
+
+// write(ctx, buffer, offset, data: TypedArray) (Compute.write, gpu.ts:32)
+napi_value write(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  CTX_ARG();
+  BUF_ARG(1, b);
+  U64_ARG(2, offset);
+  void *data = nullptr;
+  uint64_t bytes = 0;
+  if (!typed_bytes(env, argv[3], &data, &bytes)) return throw_msg(env, "WGD_E_INVALID", "data must be a typed array");
+  CHECK(c->ctx, wgd_write(c->ctx, b, offset, data, bytes));
+  return undefined(env);
+}
+
+// read(ctx, buffer, offset, out: TypedArray): fills `out` (Compute.read, gpu.ts:61-65)
+napi_value read(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  CTX_ARG();
+  BUF_ARG(1, b);
+  U64_ARG(2, offset);
+  void *data = nullptr;
+  uint64_t bytes = 0;
+  if (!typed_bytes(env, argv[3], &data, &bytes)) return throw_msg(env, "WGD_E_INVALID", "out must be a typed array");
+  CHECK(c->ctx, wgd_read(c->ctx, b, offset, data, bytes));
+  return argv[3];
+}
+
+// copy(ctx, src, dst, size, srcOffset, dstOffset) (Compute.copy, gpu.ts:52-54)
+napi_value copy(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  CTX_ARG();
+  BUF_ARG(1, src);
+  BUF_ARG(2, dst);
+  U64_ARG(3, size);
+  U64_ARG(4, so);
+  U64_ARG(5, dof);
+  CHECK(c->ctx, wgd_copy(c->ctx, src, dst, size, so, dof));
+  return undefined(env);
+}
+
+// clear(ctx, buffer) (Compute.clear, gpu.ts:55-59)
+napi_value clear(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  CTX_ARG();
+  BUF_ARG(1, b);
+  CHECK(c->ctx, wgd_clear(c->ctx, b));
+  return undefined(env);
+}
+
+// matmul(ctx, type, w, x, y, cols, rows, stride, rowBase, inputOffset, batch)
+napi_value matmul(napi_env env, napi_callback_info info) {
+  ARGS(11);
+  CTX_ARG();
+  I32_ARG(1, type);
+  BUF_ARG(2, w);
+  BUF_ARG(3, x);
+  BUF_ARG(4, y);
+  U32_ARG(5, cols);
+  U32_ARG(6, rows);
+  U32_ARG(7, stride);
+  U32_ARG(8, rowBase);
+  U32_ARG(9, inputOffset);
+  U32_ARG(10, batch);
+  CHECK(c->ctx, wgd_matmul(c->ctx, type, w, x, y, cols, rows, stride, rowBase, inputOffset, batch));
+  return undefined(env);
+}
+
+// quantizedBytes(cols) -> bytes of the quantized activation row
+napi_value quantized_bytes(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  U32_ARG(0, cols);
+  return num(env, (double)wgd_quantized_bytes(cols));
+}
+
+// quantize(ctx, x, cols, normWeight | null, epsilon, qx)
+napi_value quantize(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  CTX_ARG();
+  BUF_ARG(1, x);
+  U32_ARG(2, cols);
+  OPT_BUF_ARG(3, nw);
+  F64_ARG(4, eps);
+  BUF_ARG(5, qx);
+  CHECK(c->ctx, wgd_quantize(c->ctx, x, cols, nw, (float)eps, qx));
+  return undefined(env);
+}
+
+// matvec(ctx, type, w, qx, y, cols, rows, rowBase)
+napi_value matvec(napi_env env, napi_callback_info info) {
+  ARGS(8);
+  CTX_ARG();
+  I32_ARG(1, type);
+  BUF_ARG(2, w);
+  BUF_ARG(3, qx);
+  BUF_ARG(4, y);
+  U32_ARG(5, cols);
+  U32_ARG(6, rows);
+  U32_ARG(7, rowBase);
+  CHECK(c->ctx, wgd_matvec(c->ctx, type, w, qx, y, cols, rows, rowBase));
+  return undefined(env);
+}
+
+// dequant(ctx, type, w, out, count)
+napi_value dequant(napi_env env, napi_callback_info info) {
+  ARGS(5);
+  CTX_ARG();
+  I32_ARG(1, type);
+  BUF_ARG(2, w);
+  BUF_ARG(3, out);
+  U64_ARG(4, count);
+  CHECK(c->ctx, wgd_dequant(c->ctx, type, w, out, count));
+  return undefined(env);
+}
+
+// norm(ctx, x, w, y, n, epsilon, batch)
+napi_value norm(napi_env env, napi_callback_info info) {
+  ARGS(7);
+  CTX_ARG();
+  BUF_ARG(1, x);
+  BUF_ARG(2, w);
+  BUF_ARG(3, y);
+  U32_ARG(4, n);
+  F64_ARG(5, eps);
+  U32_ARG(6, batch);
+  CHECK(c->ctx, wgd_norm(c->ctx, x, w, y, n, (float)eps, batch));
+  return undefined(env);
+}
+
+// ropeNorm(ctx, x, w, heads, headDim, start, theta, scale, epsilon, rotaryDim, batch)
+napi_value rope_norm(napi_env env, napi_callback_info info) {
+  ARGS(11);
+  CTX_ARG();
+  BUF_ARG(1, x);
+  BUF_ARG(2, w);
+  U32_ARG(3, heads);
+  U32_ARG(4, hd);
+  U32_ARG(5, start);
+  F64_ARG(6, theta);
+  F64_ARG(7, scale);
+  F64_ARG(8, eps);
+  U32_ARG(9, rot);
+  U32_ARG(10, batch);
+  CHECK(c->ctx, wgd_rope_norm(c->ctx, x, w, heads, hd, start, (float)theta, (float)scale, (float)eps, rot, batch));
+  return undefined(env);
+}
+
+// ropeNeox / ropeAdjacent(ctx, x, heads, headDim, start, theta, scale, rotaryDim, batch)
+template <int ADJ>
+napi_value rope_plain(napi_env env, napi_callback_info info) {
+  ARGS(9);
+  CTX_ARG();
+  BUF_ARG(1, x);
+  U32_ARG(2, heads);
+  U32_ARG(3, hd);
+  U32_ARG(4, start);
+  F64_ARG(5, theta);
+  F64_ARG(6, scale);
+  U32_ARG(7, rot);
+  U32_ARG(8, batch);
+  if (ADJ) CHECK(c->ctx, wgd_rope_adjacent(c->ctx, x, heads, hd, start, (float)theta, (float)scale, rot, batch));
+  else CHECK(c->ctx, wgd_rope_neox(c->ctx, x, heads, hd, start, (float)theta, (float)scale, rot, batch));
+  return undefined(env);
+}
+
+// attention / attentionNoalloc(ctx, q, k, v, y, heads, kvHeads, headDim, start, scale,
+// window, capacity, context, batch)
+template <int NOALLOC>
+napi_value attention(napi_env env, napi_callback_info info) {
+  ARGS(14);
+  CTX_ARG();
+  BUF_ARG(1, q);
+  BUF_ARG(2, k);
+  BUF_ARG(3, v);
+  BUF_ARG(4, y);
+  U32_ARG(5, heads);
+  U32_ARG(6, kvHeads);
+  U32_ARG(7, hd);
+  U32_ARG(8, start);
+  F64_ARG(9, scale);
+  U32_ARG(10, window);
+  U32_ARG(11, capacity);
+  U32_ARG(12, context);
+  U32_ARG(13, batch);
+  if (NOALLOC)
+    CHECK(c->ctx, wgd_attention_noalloc(c->ctx, q, k, v, y, heads, kvHeads, hd, start, (float)scale, window, capacity, context, batch));
+  else
+    CHECK(c->ctx, wgd_attention(c->ctx, q, k, v, y, heads, kvHeads, hd, start, (float)scale, window, capacity, context, batch));
+  return undefined(env);
+}
+
+// add(ctx, delta, state, n)
+napi_value add(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  CTX_ARG();
+  BUF_ARG(1, delta);
+  BUF_ARG(2, state);
+  U32_ARG(3, n);
+  CHECK(c->ctx, wgd_add(c->ctx, delta, state, n));
+  return undefined(env);
+}
+
+// silu / gelu(ctx, gate, up, y, n)
+template <int GELU>
+napi_value glu(napi_env env, napi_callback_info info) {
+  ARGS(5);
+  CTX_ARG();
+  BUF_ARG(1, g);
+  BUF_ARG(2, u);
+  BUF_ARG(3, y);
+  U32_ARG(4, n);
+  if (GELU) CHECK(c->ctx, wgd_gelu(c->ctx, g, u, y, n));
+  else CHECK(c->ctx, wgd_silu(c->ctx, g, u, y, n));
+  return undefined(env);
+}
+
+// biasAdd(ctx, y, b, n, width)
+napi_value bias_add(napi_env env, napi_callback_info info) {
+  ARGS(5);
+  CTX_ARG();
+  BUF_ARG(1, y);
+  BUF_ARG(2, b);
+  U32_ARG(3, n);
+  U32_ARG(4, width);
+  CHECK(c->ctx, wgd_bias_add(c->ctx, y, b, n, width));
+  return undefined(env);
+}
+
+// activate(ctx, x, n)
+napi_value activate(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  CTX_ARG();
+  BUF_ARG(1, x);
+  U32_ARG(2, n);
+  CHECK(c->ctx, wgd_activate(c->ctx, x, n));
+  return undefined(env);
+}
+
+// argmax(ctx, logits, n, out | null) -> index of the first finite maximum
+napi_value argmax(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  CTX_ARG();
+  BUF_ARG(1, logits);
+  U32_ARG(2, n);
+  OPT_BUF_ARG(3, out);
+  int32_t id = -1;
+  CHECK(c->ctx, wgd_argmax(c->ctx, logits, n, out, &id));
+  napi_value r;
+  napi_create_int32(env, id, &r);
+  return r;
+}
+
+// sample(ctx, logits, n, temperature, topK, topP, seedHi, seedLo, index) -> token
+napi_value sample(napi_env env, napi_callback_info info) {
+  ARGS(9);
+  CTX_ARG();
+  BUF_ARG(1, logits);
+  U32_ARG(2, n);
+  F64_ARG(3, temperature);
+  U32_ARG(4, topK);
+  F64_ARG(5, topP);
+  U32_ARG(6, seedHi);
+  U32_ARG(7, seedLo);
+  U32_ARG(8, index);
+  int32_t tok = -1;
+  CHECK(c->ctx, wgd_sample(c->ctx, logits, n, temperature, topK, topP, ((uint64_t)seedHi << 32) | seedLo, index, &tok));
+  napi_value r;
+  napi_create_int32(env, tok, &r);
+  return r;
+}
+
+// embed(ctx, type, table, ids, out, hidden, n, scale)
+napi_value embed(napi_env env, napi_callback_info info) {
+  ARGS(8);
+  CTX_ARG();
+  I32_ARG(1, type);
+  BUF_ARG(2, table);
+  BUF_ARG(3, ids);
+  BUF_ARG(4, out);
+  U32_ARG(5, hidden);
+  U32_ARG(6, n);
+  F64_ARG(7, scale);
+  CHECK(c->ctx, wgd_embed(c->ctx, type, table, ids, out, hidden, n, scale));
+  return undefined(env);
+}
+
 napi_value init(napi_env env, napi_value exports) {
   const struct { const char *name; napi_callback cb; } fns[] = {
       {"create", create}, {"destroy", destroy}, {"adapterName", adapter_name}, {"memory", memory},
       {"done", done}, {"modelCreate", model_create}, {"modelTensor", model_tensor},
       {"modelReady", model_ready}, {"modelForward", model_forward}, {"modelDecode", model_decode},
-      {"modelSampling", model_sampling}, {"modelDestroy", model_destroy}};
+      {"modelSampling", model_sampling}, {"modelDestroy", model_destroy},
+      {"bufferCreate", buffer_create}, {"bufferDestroy", buffer_destroy}, {"bufferSize", buffer_size},
+      {"uploadWeights", upload_weights}, {"write", write}, {"read", read}, {"copy", copy}, {"clear", clear},
+      {"matmul", matmul}, {"quantizedBytes", quantized_bytes}, {"quantize", quantize}, {"matvec", matvec},
+      {"dequant", dequant}, {"norm", norm}, {"ropeNorm", rope_norm}, {"ropeNeox", rope_plain<0>},
+      {"ropeAdjacent", rope_plain<1>}, {"attention", attention<0>}, {"attentionNoalloc", attention<1>},
+      {"add", add}, {"silu", glu<0>}, {"gelu", glu<1>}, {"biasAdd", bias_add}, {"activate", activate},
+      {"argmax", argmax}, {"sample", sample}, {"embed", embed}};
   for (auto &f : fns) {
     napi_value fn;
     napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);
