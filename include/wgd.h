@@ -154,6 +154,20 @@ int wgd_attention_noalloc(wgd_context *ctx, const wgd_buffer *q, const wgd_buffe
                           const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads,
                           uint32_t head_dim, uint32_t start, float scale, uint32_t window,
                           uint32_t capacity, uint32_t context, uint32_t batch);
+/* wgd_attention over an f16 K/V ring: the same arguments and semantics, with k and v
+ * holding [capacity][kvHeads][hd] IEEE halves (2 bytes per element) instead of f32. Scores,
+ * softmax and the weighted sum run in f32 on the exactly widened values. The reference
+ * allocates its rings at 4 bytes per element (engine.ts:98-101, sized by attentionMemory,
+ * context.ts:16-24); the f16 ring halves that memory and the bytes each decode step reads. */
+int wgd_attention_f16kv(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k,
+                        const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads,
+                        uint32_t head_dim, uint32_t start, float scale, uint32_t window,
+                        uint32_t capacity, uint32_t context, uint32_t batch);
+/* cacheKV's ring copy (engine.ts:120-124, Compute.copy of cacheCopies' ranges) into an f16
+ * ring: dst[dst_offset + i] = f16(src[src_offset + i]) for i < count, rounded to nearest
+ * (ties to even). Offsets and count are in elements (floats of src, halves of dst). */
+int wgd_kv_store_f16(wgd_context *ctx, const wgd_buffer *src, wgd_buffer *dst, uint64_t count,
+                     uint64_t src_offset, uint64_t dst_offset);
 /* Floats of the static scratch of wgd_attention_noalloc (8 Mi floats, 32 MiB). */
 uint64_t wgd_attention_noalloc_limit(void);
 /* addShader (shaders.ts:123-128): state += delta. */
@@ -217,10 +231,12 @@ typedef struct wgd_model_config {
   int32_t batch;          /* LoadOptions.batchSize: largest forward() chunk                 */
   float epsilon, theta, local_theta, attention_scale, rope_scale;
   double embed_scale;     /* sqrt(hidden) for gemma3, 1 otherwise (engine.ts:143)          */
+  int32_t kv_f16;         /* K/V rings in f16 (1) or f32 as the reference (0, engine.ts:98-101);
+                             f16 rings store values rounded to nearest even, math stays f32 */
 } wgd_model_config;
 
 /* Allocate work buffers and per-layer K/V rings (capacities[l] slots each, from
- * attentionMemory, context.ts:16-24). */
+ * attentionMemory, context.ts:16-24; 4 bytes per element, 2 with kv_f16). */
 int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_t *capacities,
                      wgd_model **out);
 /* Upload one GGUF tensor (raw block bytes as stored in the file, `bytes` long).

@@ -24,6 +24,19 @@ double orc_half(uint16_t h) {
   return sign * ldexp(1.0, exponent - 15) * (1.0 + fraction / 1024.0);
 }
 
+/* Round to binary16: 11 significant bits for |x| >= 2^-14, a fixed 2^-24 step below
+ * (subnormals); nearbyint rounds ties to even in the default rounding mode. Values at or
+ * past 65520 (half an ulp above the largest half, 65504) overflow to infinity. */
+double orc_round_f16(double x) {
+  if (x == 0 || isnan(x) || isinf(x)) return x;
+  const double a = fabs(x);
+  if (a >= 65520.0) return x > 0 ? INFINITY : -INFINITY;
+  int e;
+  frexp(a, &e);                                  /* a = m * 2^e, 0.5 <= m < 1 */
+  const double ulp = e - 1 >= -14 ? ldexp(1.0, e - 11) : ldexp(1.0, -24);
+  return copysign(nearbyint(a / ulp) * ulp, x);
+}
+
 static double f16at(const uint8_t *b, int64_t p) { return orc_half((uint16_t)(b[p] | (b[p + 1] << 8))); }
 
 /* decodeWeight, src/core/quant.ts:6-29: one element, literal restatement. */
@@ -357,6 +370,11 @@ int orc_model_forward(orc_model *m, const int32_t *ids, int32_t n, int32_t start
       int64_t slot = ((int64_t)start + b) % cap;
       memcpy(m->kcache[l] + slot * kd, k + b * kd, sizeof(double) * kd);
       memcpy(m->vcache[l] + slot * kd, v + b * kd, sizeof(double) * kd);
+      if (c->kv_f16)
+        for (int64_t i = 0; i < kd; i++) {
+          m->kcache[l][slot * kd + i] = orc_round_f16(m->kcache[l][slot * kd + i]);
+          m->vcache[l][slot * kd + i] = orc_round_f16(m->vcache[l][slot * kd + i]);
+        }
     }
     orc_attention(q, m->kcache[l], m->vcache[l], att, c->heads, c->kv_heads, hd, start,
                   c->attention_scale, window, cap, n);

@@ -46,6 +46,8 @@ void orc_attention(const double *q, const double *k, const double *v, double *y,
                    int64_t kv_heads, int64_t hd, int64_t start, double scale, int64_t window,
                    int64_t capacity, int64_t batch);
 int64_t orc_argmax(const float *logits, int64_t n);
+/* x rounded to the nearest IEEE binary16 value (ties to even; overflow to +-inf), as f64. */
+double orc_round_f16(double x);
 
 typedef struct orc_config {
   int32_t family, rope_adjacent;
@@ -54,6 +56,7 @@ typedef struct orc_config {
   int32_t qk_norm, ffn_gate, gelu, bias_q, bias_k, bias_v, bias_output, tied_output;
   int32_t context, batch;
   double epsilon, theta, local_theta, attention_scale, rope_scale, embed_scale;
+  int32_t kv_f16; /* K/V ring values rounded to the nearest f16 (ties to even) when cached */
 } orc_config;
 
 typedef struct orc_model orc_model;

@@ -50,12 +50,18 @@ def lib() -> C.CDLL:
         l.orc_model_forward.restype = C.c_int; l.orc_model_forward.argtypes = [_P, C.POINTER(_I32), _I32, _I32, _P]
         l.orc_model_destroy.restype = None; l.orc_model_destroy.argtypes = [_P]
         l.orc_threads.restype = C.c_int; l.orc_threads.argtypes = []
+        l.orc_round_f16.restype = _D; l.orc_round_f16.argtypes = [_D]
         _lib = l
     return _lib
 
 
 def _ptr(a: np.ndarray) -> int:
     return a.ctypes.data
+
+
+def round_f16(x: float) -> float:
+    """x rounded to the nearest binary16 value (ties to even), as a float."""
+    return lib().orc_round_f16(x)
 
 
 def half(h: int) -> float:
@@ -178,10 +184,10 @@ class OrcConfig(C.Structure):
         "family", "rope_adjacent", "hidden", "intermediate", "layers", "heads", "kv_heads", "head_dim", "vocab",
         "rotary_dim", "window", "period", "qk_norm", "ffn_gate", "gelu", "bias_q", "bias_k", "bias_v",
         "bias_output", "tied_output", "context", "batch")] + [(n, C.c_double) for n in (
-        "epsilon", "theta", "local_theta", "attention_scale", "rope_scale", "embed_scale")]
+        "epsilon", "theta", "local_theta", "attention_scale", "rope_scale", "embed_scale")] + [("kv_f16", C.c_int32)]
 
 
-def config_struct(gguf, cfg, context: int) -> OrcConfig:
+def config_struct(gguf, cfg, context: int, kv_f16: bool = False) -> OrcConfig:
     """The oracle's orc_config for a parsed GGUF and its model config."""
     c = OrcConfig()
     gemma = cfg.family == "gemma3"
@@ -201,16 +207,18 @@ def config_struct(gguf, cfg, context: int) -> OrcConfig:
     c.epsilon, c.theta, c.local_theta = cfg.epsilon, cfg.theta, cfg.localTheta
     c.attention_scale, c.rope_scale = cfg.attentionScale, cfg.ropeScale
     c.embed_scale = math.sqrt(cfg.hidden) if cfg.architecture == "gemma3" else 1.0
+    c.kv_f16 = 1 if kv_f16 else 0
     return c
 
 
 class OracleModel:
     """The f64 reference forward over the raw bytes of a GGUF file."""
 
-    def __init__(self, file: np.ndarray, gguf, cfg, context: int, capacities: Sequence[int]) -> None:
+    def __init__(self, file: np.ndarray, gguf, cfg, context: int, capacities: Sequence[int],
+                 kv_f16: bool = False) -> None:
         self.file = np.ascontiguousarray(file, np.uint8)
         self.cfg = cfg
-        c = config_struct(gguf, cfg, context)
+        c = config_struct(gguf, cfg, context, kv_f16)
         caps = (C.c_int32 * cfg.layers)(*capacities)
         self.m = lib().orc_model_create(C.byref(c), caps)
         base = self.file.ctypes.data

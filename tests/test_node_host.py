@@ -66,7 +66,8 @@ NODE_EXPORTS = ["create", "destroy", "adapterName", "memory", "done", "modelCrea
                 "modelForward", "modelDecode", "modelSampling", "modelDestroy", "bufferCreate", "bufferDestroy",
                 "bufferSize", "uploadWeights", "write", "read", "copy", "clear", "matmul", "quantizedBytes",
                 "quantize", "matvec", "dequant", "norm", "ropeNorm", "ropeNeox", "ropeAdjacent", "attention",
-                "attentionNoalloc", "add", "silu", "gelu", "biasAdd", "activate", "argmax", "sample", "embed"]
+                "attentionNoalloc", "attentionF16kv", "kvStoreF16", "add", "silu", "gelu", "biasAdd", "activate",
+                "argmax", "sample", "embed"]
 
 
 @needs_node

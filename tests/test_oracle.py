@@ -31,6 +31,23 @@ def test_half_matches_ieee_for_every_pattern():
     assert np.array_equal(ref[~both_nan], got[~both_nan]) and np.array_equal(np.isnan(ref), np.isnan(got))
 
 
+def test_round_f16_matches_ieee_conversion():
+    """The f16 K/V ring's rounding (orc_round_f16) against numpy's IEEE binary16 conversion:
+    random magnitudes over the whole range, every midpoint between adjacent halves (ties go
+    to the even one), the subnormal step and overflow."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(40000) * 10.0 ** rng.integers(-10, 6, 40000)
+    h = np.arange(0, 0x7BFF, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = (h[:-1] + h[1:]) / 2
+    x = np.concatenate([x, mids, -mids, [65504.0, 65519.99, 65520.0, 1e6, 2.0 ** -25, 2.0 ** -26, 0.0, math.inf]])
+    got = np.array([orc.round_f16(float(v)) for v in x])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float64)
+    assert np.array_equal(got, want)
+    # a dropped tie rule shows: 1 + 2^-11 sits halfway between 1 and 1 + 2^-10
+    assert orc.round_f16(1 + 2.0 ** -11) == 1.0 and orc.round_f16(1 + 3 * 2.0 ** -11) == 1 + 2.0 ** -9
+
+
 # ---------------------------------------------------------------- quant.test.ts:11-18
 def test_q4_0_and_q8_0_signed_blocks_across_block_boundary():
     q4 = np.zeros(36, np.uint8)

@@ -33,9 +33,10 @@ def output_limit(requested, prompt_tokens: int, context: int) -> int:
     return int(min(requested, context - prompt_tokens))
 
 
-def attention_memory(c, context: int, batch: int) -> Dict[str, object]:
+def attention_memory(c, context: int, batch: int, element_bytes: int = 4) -> Dict[str, object]:
     """Per-layer ring capacities: Gemma local layers and sliding-window models keep the
-    window plus the rest of the current prompt batch (context.ts:14-19)."""
+    window plus the rest of the current prompt batch (context.ts:14-19). kvBytes counts
+    K and V at ``element_bytes`` each: 4 as the reference's f32 rings, 2 for f16 rings."""
     caps: List[int] = []
     for l in range(c.layers):
         if c.family == "gemma3":
@@ -44,7 +45,7 @@ def attention_memory(c, context: int, batch: int) -> Dict[str, object]:
             caps.append(min(context, c.slidingWindow + batch - 1))
         else:
             caps.append(context)
-    kv_bytes = sum(caps) * c.kvHeads * c.headDim * 8
+    kv_bytes = sum(caps) * c.kvHeads * c.headDim * 2 * element_bytes
     return {"capacities": caps, "kvBytes": kv_bytes, "stateBytes": 0, "totalBytes": kv_bytes}
 
 

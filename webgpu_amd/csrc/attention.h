@@ -13,7 +13,8 @@ namespace wgd {
 // written as f32 y[heads * hd] and, when qx.d0 is set, quantized for the O projection.
 struct DecodeAttnArgs {
   const float *q, *k, *v;        // projections of the token, before RoPE: [heads][hd], [kvh][hd]
-  float *kc, *vc;                // ring [capacity][kvh][hd]
+  void *kc, *vc;                 // ring [capacity][kvh][hd], f32 or (kv16) f16
+  bool kv16 = false;
   const float *q_norm, *k_norm;  // mode 0 weights
   float *partial;                // decode_attention_scratch_floats()
   float *y;

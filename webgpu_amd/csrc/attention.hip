@@ -19,7 +19,7 @@
 namespace wgd {
 
 struct AttnK {
-  const float *q, *k, *v; float *y, *part;
+  const float *q; const void *k, *v; float *y, *part;  // k, v: ring of E elements
   uint32_t heads, kvh, hd, start; const int32_t *start_dev;
   float scale; uint32_t window, capacity, batch;
   uint32_t qb, nsplit, T, R, group;
@@ -33,6 +33,7 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+template <class E>
 __global__ __launch_bounds__(256) void k_attention(AttnK a) {
   extern __shared__ float lds[];
   const uint32_t hd = a.hd, T = a.T, R = a.R, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnK a) {
       float kvk = 0.f, kvv = 0.f;
       if (t < hi) {
         uint64_t src = ((uint64_t)(t % a.capacity) * a.kvh + kv) * hd + d;
-        kvk = a.k[src]; kvv = a.v[src];
+        kvk = kv_get<E>(a.k, src); kvv = kv_get<E>(a.v, src);
       }
       Ks[j * (hd + 1) + d] = kvk;
       Vs[j * hd + d] = kvv;
@@ -190,7 +191,7 @@ constexpr uint32_t AP_T = 64;  // keys per LDS tile
 template <uint32_t HD>
 constexpr size_t attn_prompt_lds() { return sizeof(float) * ((size_t)AP_T * (HD + 4) + (size_t)HD * (AP_T + 4)); }
 
-template <uint32_t HD>
+template <uint32_t HD, class E>
 __global__ __launch_bounds__(256) void k_attn_prompt(AttnK a) {
   constexpr uint32_t T = AP_T, KS = HD + 4, VS = T + 4, NT = HD / 16;
   extern __shared__ float lds[];
@@ -233,8 +234,9 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnK a) {
       f32x4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
       if (t < hi) {
         const uint64_t src = ((uint64_t)(t % a.capacity) * a.kvh + kv) * HD + d;
-        kk = *(const f32x4 *)(a.k + src);
-        vv = *(const f32x4 *)(a.v + src);
+        const float4 k4 = kv_get4<E>(a.k, src), v4 = kv_get4<E>(a.v, src);
+        kk = f32x4{k4.x, k4.y, k4.z, k4.w};
+        vv = f32x4{v4.x, v4.y, v4.z, v4.w};
       }
       *(f32x4 *)(Ks + j * KS + d) = kk;
       Vt[(d + 0) * VS + j] = vv.x;
@@ -322,13 +324,13 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnK a) {
   }
 }
 
-template <uint32_t HD>
+template <uint32_t HD, class E>
 static hipError_t launch_attn_prompt(hipStream_t s, AttnK a, const AttnArgs &in, uint32_t nsplit) {
   const uint32_t nqt = (in.batch + 15) / 16;
   a.nsplit = nsplit;
   constexpr size_t lds = attn_prompt_lds<HD>();
-  if (lds > 65536) lds_opt_in((const void *)k_attn_prompt<HD>);
-  hipLaunchKernelGGL(k_attn_prompt<HD>, dim3(in.kv_heads, (nqt * a.group + 3) / 4, nsplit), dim3(256), lds, s, a);
+  if (lds > 65536) lds_opt_in((const void *)k_attn_prompt<HD, E>);
+  hipLaunchKernelGGL((k_attn_prompt<HD, E>), dim3(in.kv_heads, (nqt * a.group + 3) / 4, nsplit), dim3(256), lds, s, a);
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
     uint16_t *xs = in.xs && in.hd % 8 == 0 && in.heads * in.hd % 64 == 0 ? in.xs : nullptr;
@@ -414,16 +416,21 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
   a.group = in.heads / in.kv_heads;
   AttnPlan p;
   if (!attn_plan(in, in.partial ? in.partial_floats : 0, p)) return hipErrorInvalidValue;
-  if (p.mfma_hd == 64) return launch_attn_prompt<64>(s, a, in, p.nsplit);
-  if (p.mfma_hd == 128) return launch_attn_prompt<128>(s, a, in, p.nsplit);
-  if (p.mfma_hd == 256) return launch_attn_prompt<256>(s, a, in, p.nsplit);
+  if (p.mfma_hd == 64) return in.kv16 ? launch_attn_prompt<64, _Float16>(s, a, in, p.nsplit) : launch_attn_prompt<64, float>(s, a, in, p.nsplit);
+  if (p.mfma_hd == 128) return in.kv16 ? launch_attn_prompt<128, _Float16>(s, a, in, p.nsplit) : launch_attn_prompt<128, float>(s, a, in, p.nsplit);
+  if (p.mfma_hd == 256) return in.kv16 ? launch_attn_prompt<256, _Float16>(s, a, in, p.nsplit) : launch_attn_prompt<256, float>(s, a, in, p.nsplit);
   a.qb = p.qb; a.R = p.R; a.T = p.T;
   const uint32_t qblocks = p.qblocks, nsplit = p.nsplit;
   a.nsplit = nsplit;
   size_t lds = sizeof(float) * ((size_t)a.T * (in.hd + 1) + (size_t)a.T * in.hd + (size_t)a.R * in.hd +
                                 (size_t)a.R * a.T + 3 * a.R);
-  if (lds > 65536) lds_opt_in((const void *)k_attention);
-  hipLaunchKernelGGL(k_attention, dim3(in.kv_heads, qblocks, nsplit), dim3(256), lds, s, a);
+  if (in.kv16) {
+    if (lds > 65536) lds_opt_in((const void *)k_attention<_Float16>);
+    hipLaunchKernelGGL(k_attention<_Float16>, dim3(in.kv_heads, qblocks, nsplit), dim3(256), lds, s, a);
+  } else {
+    if (lds > 65536) lds_opt_in((const void *)k_attention<float>);
+    hipLaunchKernelGGL(k_attention<float>, dim3(in.kv_heads, qblocks, nsplit), dim3(256), lds, s, a);
+  }
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
     hipLaunchKernelGGL(k_attention_combine, dim3(in.batch * in.heads), dim3(128), 0, s, (const float *)in.partial,
@@ -449,7 +456,7 @@ constexpr uint32_t AD_KPB = 8;   // keys per wavefront batch
 constexpr uint32_t AD_WAVES = 4;
 
 struct AttnDecK {
-  const float *q, *k, *v; float *kc, *vc; const float *qn, *kn; float *part;
+  const float *q, *k, *v; void *kc, *vc; const float *qn, *kn; float *part;  // kc, vc: ring of E elements
   const int32_t *pos;
   const float *cs;   // this token's rotation: cos of pair i at [i], sin at [rot / 2 + i]
   uint32_t heads, kvh, rot, cap, window, group, chunk, nsplit;
@@ -481,7 +488,7 @@ __device__ __forceinline__ void chunk_epilogue(const AttnDecK &a, uint32_t kv, u
   }
 }
 
-template <int EL, int G>
+template <int EL, int G, class E>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
   constexpr uint32_t HD = 64 * EL;
   __shared__ float vec[(G + 1) * HD];        // query heads, then the new key
@@ -506,7 +513,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
       if (t >= hi) t = lo;
       const uint64_t base = (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD + lane * EL;
 #pragma unroll
-      for (int e = 0; e < EL; e++) { kr[k][e] = a.kc[base + e]; vr[k][e] = a.vc[base + e]; }
+      for (int e = 0; e < EL; e++) { kr[k][e] = kv_get<E>(a.kc, base + e); vr[k][e] = kv_get<E>(a.vc, base + e); }
     }
   };
   load_batch(0);
@@ -546,8 +553,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
   if (mine) {
     const uint64_t slot = (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
     for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x) {
-      a.kc[slot + d] = vec[g * HD + d];
-      a.vc[slot + d] = a.v[(uint64_t)kv * HD + d];
+      kv_put(a.kc, slot + d, vec[g * HD + d], sizeof(E) == 2);
+      kv_put(a.vc, slot + d, a.v[(uint64_t)kv * HD + d], sizeof(E) == 2);
     }
   }
   float qr[G][EL], kf[EL], vf[EL];
@@ -556,7 +563,10 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
 #pragma unroll
     for (int e = 0; e < EL; e++) qr[i][e] = (uint32_t)i < g ? vec[i * HD + lane * EL + e] : 0.f;
 #pragma unroll
-  for (int e = 0; e < EL; e++) { kf[e] = vec[g * HD + lane * EL + e]; vf[e] = a.v[(uint64_t)kv * HD + lane * EL + e]; }
+  for (int e = 0; e < EL; e++) {
+    kf[e] = (float)(E)vec[g * HD + lane * EL + e];
+    vf[e] = (float)(E)a.v[(uint64_t)kv * HD + lane * EL + e];
+  }
   // ---- keys
   float m[G], l[G], o[G][EL];
 #pragma unroll
@@ -657,7 +667,7 @@ __device__ __forceinline__ float slots_reduce(float v) {
   return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <uint32_t HD, int G, bool ADJ>
+template <uint32_t HD, int G, bool ADJ, class E>
 __global__ __launch_bounds__(256) void k_attn_dec2(AttnDecK a) {
   constexpr uint32_t LPK = HD / 8, KPW = 64 / LPK, NW = AD_WAVES;
   __shared__ float wm[AD_WAVES][G], wl[AD_WAVES][G];
@@ -710,9 +720,9 @@ __global__ __launch_bounds__(256) void k_attn_dec2(AttnDecK a) {
     for (uint32_t d = 0; d < AD2_DB; d++) {
       uint32_t t = key_of(b, d);
       if (t >= hi) t = lo;  // masked below; any valid row
-      const float *kr = a.kc + (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD, *vr = a.vc + (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD;
-      kb[d][0] = *(const float4 *)(kr + e0); kb[d][1] = *(const float4 *)(kr + e1);
-      vb[d][0] = *(const float4 *)(vr + e0); vb[d][1] = *(const float4 *)(vr + e1);
+      const uint64_t r = (uint64_t)(t % a.cap) * rowf + (uint64_t)kv * HD;
+      kb[d][0] = kv_get4<E>(a.kc, r + e0); kb[d][1] = kv_get4<E>(a.kc, r + e1);
+      vb[d][0] = kv_get4<E>(a.vc, r + e0); vb[d][1] = kv_get4<E>(a.vc, r + e1);
     }
   };
   load_batch(0);
@@ -749,10 +759,15 @@ __global__ __launch_bounds__(256) void k_attn_dec2(AttnDecK a) {
 #pragma unroll
   for (int i = 0; i < G; i++) rot(q[i]);
   rot(kn);
+  if (sizeof(E) == 2) {
+    // the new key and value as the f16 ring holds them, so every chunk sees the same values
+    auto rnd = [](float4 &v) { v = make_float4((float)(E)v.x, (float)(E)v.y, (float)(E)v.z, (float)(E)v.w); };
+    rnd(kn[0]); rnd(kn[1]); rnd(vn[0]); rnd(vn[1]);
+  }
   if (pos >= lo && pos < hi && w == 0 && slot == 0) {
-    float *ks = a.kc + (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD, *vs = a.vc + (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
-    *(float4 *)(ks + e0) = kn[0]; *(float4 *)(ks + e1) = kn[1];
-    *(float4 *)(vs + e0) = vn[0]; *(float4 *)(vs + e1) = vn[1];
+    const uint64_t r = (uint64_t)(pos % a.cap) * rowf + (uint64_t)kv * HD;
+    kv_put4<E>(a.kc, r + e0, kn[0]); kv_put4<E>(a.kc, r + e1, kn[1]);
+    kv_put4<E>(a.vc, r + e0, vn[0]); kv_put4<E>(a.vc, r + e1, vn[1]);
   }
   // ---- keys
   float m[G], l[G];
@@ -943,20 +958,29 @@ static uint32_t dec2_chunk(uint32_t capacity, uint32_t kvh, uint32_t hd) {
   return c;
 }
 
-template <int EL>
+template <int EL, class E>
 static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid) {
-  if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec<EL, 1>), grid, dim3(256), 0, s, k);
-  else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec<EL, 2>), grid, dim3(256), 0, s, k);
-  else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec<EL, 4>), grid, dim3(256), 0, s, k);
-  else hipLaunchKernelGGL((k_attn_dec<EL, 8>), grid, dim3(256), 0, s, k);
+  if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec<EL, 1, E>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec<EL, 2, E>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec<EL, 4, E>), grid, dim3(256), 0, s, k);
+  else hipLaunchKernelGGL((k_attn_dec<EL, 8, E>), grid, dim3(256), 0, s, k);
+}
+template <int EL>
+static void launch_dec(hipStream_t s, const AttnDecK &k, dim3 grid, bool kv16) {
+  kv16 ? launch_dec<EL, _Float16>(s, k, grid) : launch_dec<EL, float>(s, k, grid);
 }
 
-template <uint32_t HD, bool ADJ>
+template <uint32_t HD, bool ADJ, class E>
 static void launch_dec2(hipStream_t s, const AttnDecK &k, dim3 grid) {
-  if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec2<HD, 1, ADJ>), grid, dim3(256), 0, s, k);
-  else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec2<HD, 2, ADJ>), grid, dim3(256), 0, s, k);
-  else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec2<HD, 4, ADJ>), grid, dim3(256), 0, s, k);
-  else hipLaunchKernelGGL((k_attn_dec2<HD, 8, ADJ>), grid, dim3(256), 0, s, k);
+  if (k.group <= 1) hipLaunchKernelGGL((k_attn_dec2<HD, 1, ADJ, E>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 2) hipLaunchKernelGGL((k_attn_dec2<HD, 2, ADJ, E>), grid, dim3(256), 0, s, k);
+  else if (k.group <= 4) hipLaunchKernelGGL((k_attn_dec2<HD, 4, ADJ, E>), grid, dim3(256), 0, s, k);
+  else hipLaunchKernelGGL((k_attn_dec2<HD, 8, ADJ, E>), grid, dim3(256), 0, s, k);
+}
+template <uint32_t HD>
+static void launch_dec2(hipStream_t s, const AttnDecK &k, dim3 grid, bool adj, bool kv16) {
+  if (kv16) adj ? launch_dec2<HD, true, _Float16>(s, k, grid) : launch_dec2<HD, false, _Float16>(s, k, grid);
+  else adj ? launch_dec2<HD, true, float>(s, k, grid) : launch_dec2<HD, false, float>(s, k, grid);
 }
 
 hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
@@ -978,12 +1002,12 @@ hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
   const dim3 grid(in.kv_heads, k.nsplit);
   if (full) {
     const bool adj = in.mode == 2;
-    if (in.hd == 64) adj ? launch_dec2<64, true>(s, k, grid) : launch_dec2<64, false>(s, k, grid);
-    else if (in.hd == 128) adj ? launch_dec2<128, true>(s, k, grid) : launch_dec2<128, false>(s, k, grid);
-    else adj ? launch_dec2<256, true>(s, k, grid) : launch_dec2<256, false>(s, k, grid);
-  } else if (in.hd == 64) launch_dec<1>(s, k, grid);
-  else if (in.hd == 128) launch_dec<2>(s, k, grid);
-  else launch_dec<4>(s, k, grid);
+    if (in.hd == 64) launch_dec2<64>(s, k, grid, adj, in.kv16);
+    else if (in.hd == 128) launch_dec2<128>(s, k, grid, adj, in.kv16);
+    else launch_dec2<256>(s, k, grid, adj, in.kv16);
+  } else if (in.hd == 64) launch_dec<1>(s, k, grid, in.kv16);
+  else if (in.hd == 128) launch_dec<2>(s, k, grid, in.kv16);
+  else launch_dec<4>(s, k, grid, in.kv16);
   WGD_HIP(hipGetLastError());
   const uint32_t threads = (in.hd + 63) / 64 * 64;
   hipLaunchKernelGGL(k_attn_comb, dim3(in.heads), dim3(threads), 0, s, (const float *)in.partial, in.y, in.qx,

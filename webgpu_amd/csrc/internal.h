@@ -155,7 +155,8 @@ struct QKVFinish {
   const float *part = nullptr; uint32_t splits = 0, rows_total = 0, batch = 0;
   const float *bq = nullptr, *bk = nullptr, *bv = nullptr;
   const float *qn = nullptr, *kn = nullptr;  // mode 0 norm weights
-  float *q = nullptr, *kc = nullptr, *vc = nullptr; uint32_t capacity = 0;
+  float *q = nullptr; void *kc = nullptr, *vc = nullptr; uint32_t capacity = 0;
+  bool kv16 = false;  // ring elements are f16
   uint32_t heads = 0, kvh = 0, hd = 0, rot = 0, start = 0; const int32_t *start_dev = nullptr;
   float eps = 0.f; int mode = 1;
   const float2 *cs = nullptr;  // rope_table() of the batch's positions
@@ -166,12 +167,13 @@ hipError_t qkv_finish(hipStream_t s, const QKVFinish &a);
 hipError_t rope_table(hipStream_t s, float2 *cs, uint32_t rot, uint32_t n, uint32_t start, const int32_t *start_dev,
                       float theta, float scale);
 struct AttnArgs {
-  const float *q; const float *k; const float *v; float *y;
+  const float *q; const void *k; const void *v; float *y;  // k, v: the K/V ring (f32, or f16 with kv16)
   uint32_t heads, kv_heads, hd, start; const int32_t *start_dev;
   float scale; uint32_t window, capacity, batch;
   float *partial; uint32_t partial_floats;  // split-K scratch (may be null: single split)
   // optional: the output also in the prompt GEMM's split form; *xs_written says whether it was
   uint16_t *xs = nullptr; bool *xs_written = nullptr;
+  bool kv16 = false;
 };
 hipError_t attention(hipStream_t s, const AttnArgs &a);
 // Floats of split-K partials attention() writes for these arguments when its scratch does
@@ -187,10 +189,40 @@ hipError_t bias_add(hipStream_t s, float *y, const float *b, uint32_t n, uint32_
 hipError_t activate(hipStream_t s, float *x, uint32_t n);
 // argmax over finite values, first index wins; writes -1 when none is finite.
 hipError_t argmax(hipStream_t s, const float *logits, uint32_t n, int32_t *out);
-// Copies K/V rows of a batch into ring slots (start + i) % capacity.
-hipError_t kv_append(hipStream_t s, const float *k, const float *v, float *kc, float *vc,
+// Copies K/V rows of a batch into ring slots (start + i) % capacity; an f16 ring (kv16)
+// stores each value rounded to the nearest f16 (ties to even).
+hipError_t kv_append(hipStream_t s, const float *k, const float *v, void *kc, void *vc,
                      uint32_t row_floats, uint32_t n, uint32_t start, const int32_t *start_dev,
-                     uint32_t capacity);
+                     uint32_t capacity, bool kv16 = false);
+// n f32 values of src into an f16 buffer, rounded to nearest (ties to even).
+hipError_t to_f16(hipStream_t s, const float *src, _Float16 *dst, uint64_t n);
+
+#ifdef __HIPCC__
+// K/V ring elements: f32, or f16 (stored rounded to nearest even, widened exactly on load).
+template <class E> __device__ __forceinline__ float kv_get(const void *ring, uint64_t i) {
+  return (float)((const E *)ring)[i];
+}
+template <class E> __device__ __forceinline__ float4 kv_get4(const void *ring, uint64_t i) {
+  if constexpr (sizeof(E) == 4) return *(const float4 *)((const float *)ring + i);
+  const uint2 h = *(const uint2 *)((const _Float16 *)ring + i);
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 a = __builtin_bit_cast(h2, h.x), b = __builtin_bit_cast(h2, h.y);
+  return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+}
+__device__ __forceinline__ void kv_put(void *ring, uint64_t i, float x, bool f16) {
+  if (f16) ((_Float16 *)ring)[i] = (_Float16)x;
+  else ((float *)ring)[i] = x;
+}
+template <class E> __device__ __forceinline__ void kv_put4(void *ring, uint64_t i, const float4 &v) {
+  if constexpr (sizeof(E) == 4) {
+    *(float4 *)((float *)ring + i) = v;
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a = {(_Float16)v.x, (_Float16)v.y}, b = {(_Float16)v.z, (_Float16)v.w};
+    *(uint2 *)((_Float16 *)ring + i) = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+  }
+}
+#endif
 // Normalise `delta` with w (post-norm) and add into state: state += norm(delta) * w.
 hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n,
                     float eps, uint32_t batch);

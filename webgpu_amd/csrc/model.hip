@@ -34,7 +34,7 @@ struct Layer {
   float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
   float *post_attn = nullptr, *post_ffw = nullptr;
   float *bq = nullptr, *bk = nullptr, *bv = nullptr, *bo = nullptr;
-  float *kc = nullptr, *vc = nullptr;
+  void *kc = nullptr, *vc = nullptr;  // K/V rings: f32, or f16 with kv_f16
   uint32_t cap = 0;
 };
 
@@ -139,10 +139,10 @@ hipError_t attention_block(wgd_model *m, int l, uint32_t n, uint32_t start, cons
     const float *qn = r.mode == 0 ? L.q_norm : nullptr, *kn = r.mode == 0 ? L.k_norm : nullptr;
     WGD_HIP(rope(s, m->q, qn, c.heads, hd, start, start_dev, r.theta, r.scale, r.eps, r.rot, n, r.mode));
     WGD_HIP(rope(s, m->k, kn, c.kv_heads, hd, start, start_dev, r.theta, r.scale, r.eps, r.rot, n, r.mode));
-    WGD_HIP(kv_append(s, m->k, m->v, L.kc, L.vc, kd, n, start, start_dev, L.cap));
+    WGD_HIP(kv_append(s, m->k, m->v, L.kc, L.vc, kd, n, start, start_dev, L.cap, c.kv_f16 != 0));
   }
   AttnArgs a;
-  a.q = m->q; a.k = L.kc; a.v = L.vc; a.y = m->att;
+  a.q = m->q; a.k = L.kc; a.v = L.vc; a.y = m->att; a.kv16 = c.kv_f16 != 0;
   a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = hd; a.start = start; a.start_dev = start_dev;
   a.scale = c.attention_scale; a.window = window_of(m, l); a.capacity = L.cap; a.batch = n;
   a.partial = m->att_part; a.partial_floats = (uint32_t)m->att_part_floats;
@@ -156,7 +156,7 @@ hipError_t decode_attention_layer(wgd_model *m, int l, const QXOut &qx) {
   const wgd_model_config &c = m->c;
   Layer &L = m->L[l];
   DecodeAttnArgs a;
-  a.q = m->q; a.k = m->k; a.v = m->v; a.kc = L.kc; a.vc = L.vc;
+  a.q = m->q; a.k = m->k; a.v = m->v; a.kc = L.kc; a.vc = L.vc; a.kv16 = c.kv_f16 != 0;
   a.q_norm = nullptr; a.k_norm = nullptr;
   a.partial = m->att_part; a.y = m->att; a.qx = qx; a.pos = &m->state->pos;
   a.heads = c.heads; a.kv_heads = c.kv_heads; a.hd = c.head_dim; a.capacity = L.cap; a.window = window_of(m, l);
@@ -272,7 +272,7 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       f.part = gs.p; f.splits = splits; f.rows_total = qd + 2 * kd; f.batch = n;
       f.bq = L.bq; f.bk = L.bk; f.bv = L.bv;
       f.qn = r.mode == 0 ? L.q_norm : nullptr; f.kn = r.mode == 0 ? L.k_norm : nullptr;
-      f.q = m->q; f.kc = L.kc; f.vc = L.vc; f.capacity = L.cap;
+      f.q = m->q; f.kc = L.kc; f.vc = L.vc; f.capacity = L.cap; f.kv16 = c.kv_f16 != 0;
       f.heads = c.heads; f.kvh = c.kv_heads; f.hd = c.head_dim; f.rot = r.rot ? r.rot : c.head_dim;
       f.start = start; f.start_dev = start_dev;
       f.eps = r.eps; f.mode = r.mode;
@@ -538,7 +538,7 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
       c.kv_heads < 1 || c.heads % c.kv_heads || c.head_dim < 2 || c.head_dim > 512 || c.head_dim % 2 ||
       c.intermediate < 1 || c.intermediate > 131072 || c.vocab < 1 || c.vocab > 1000000 || c.rotary_dim % 2 ||
       c.rotary_dim > c.head_dim || c.context < 1 || c.batch < 1 || c.batch > 128 || c.heads / c.kv_heads > 16 ||
-      (c.family != 0 && c.family != 1) || c.window < 0 || c.period < 0)
+      (c.family != 0 && c.family != 1) || c.window < 0 || c.period < 0 || (c.kv_f16 != 0 && c.kv_f16 != 1))
     return fail(ctx, WGD_E_INVALID, "Unsupported model dimensions.");
   wgd_model *m = new wgd_model();
   m->ctx = ctx;
@@ -579,9 +579,10 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
     m->L[l].cap = (uint32_t)capacities[l];
     char label[64];
     snprintf(label, sizeof label, "K %d", l);
-    rc = alloc_t(m, (uint64_t)capacities[l] * kd, label, &m->L[l].kc);
+    const uint64_t ring = (uint64_t)capacities[l] * kd * (c.kv_f16 ? 2 : 4);
+    rc = alloc(m, ring, label, &m->L[l].kc);
     snprintf(label, sizeof label, "V %d", l);
-    rc = rc ? rc : alloc_t(m, (uint64_t)capacities[l] * kd, label, &m->L[l].vc);
+    rc = rc ? rc : alloc(m, ring, label, &m->L[l].vc);
   }
   if (rc) { std::string e = ctx->error; model_destroy(m); ctx->error = e; return rc; }
   *out = m;

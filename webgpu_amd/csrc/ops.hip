@@ -305,9 +305,12 @@ __global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
   __builtin_amdgcn_wave_barrier();
   const uint32_t s0 = a.start_dev ? (uint32_t)*a.start_dev : a.start;
   const uint64_t ring = (uint64_t)((s0 + tok) % a.capacity) * a.kvh * hd + (uint64_t)h * hd;
-  float *dst = kind == 0 ? a.q + ((uint64_t)tok * a.heads + h) * hd : kind == 1 ? a.kc + ring : a.vc + ring;
+  // Q rows go to q (f32); K/V rows to the ring (f32, or f16 rounded to nearest even)
+  void *dst = kind == 0 ? (void *)(a.q + ((uint64_t)tok * a.heads + h) * hd) : kind == 1 ? a.kc : a.vc;
+  const uint64_t d0 = kind == 0 ? 0 : ring;
+  const bool f16 = kind != 0 && a.kv16;
   if (kind == 2) {
-    for (uint32_t d = lane; d < hd; d += 64) dst[d] = v[d];
+    for (uint32_t d = lane; d < hd; d += 64) kv_put(dst, d0 + d, v[d], f16);
     return;
   }
   const float *w = kind == 0 ? a.qn : a.kn;
@@ -325,10 +328,10 @@ __global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
     const uint32_t ia = a.mode == 2 ? 2 * i : i, ib = a.mode == 2 ? 2 * i + 1 : i + half;
     float x0 = v[ia], x1 = v[ib];
     if (a.mode == 0) { x0 = x0 * w[ia] * inv; x1 = x1 * w[ib] * inv; }
-    dst[ia] = x0 * c - x1 * sf;
-    dst[ib] = x0 * sf + x1 * c;
+    kv_put(dst, d0 + ia, x0 * c - x1 * sf, f16);
+    kv_put(dst, d0 + ib, x0 * sf + x1 * c, f16);
   }
-  for (uint32_t d = a.rot + lane; d < hd; d += 64) dst[d] = a.mode == 0 ? v[d] * w[d] * inv : v[d];
+  for (uint32_t d = a.rot + lane; d < hd; d += 64) kv_put(dst, d0 + d, a.mode == 0 ? v[d] * w[d] * inv : v[d], f16);
 }
 
 hipError_t qkv_finish(hipStream_t s, const QKVFinish &a) {
@@ -426,24 +429,35 @@ hipError_t activate(hipStream_t s, float *x, uint32_t n) {
 }
 
 // ------------------------------------------------------------------ KV ring append
-__global__ void k_kv_append(const float *k, const float *v, float *kc, float *vc, uint32_t row, uint32_t n,
-                            uint32_t start, const int32_t *start_dev, uint32_t capacity) {
+__global__ void k_kv_append(const float *k, const float *v, void *kc, void *vc, uint32_t row, uint32_t n,
+                            uint32_t start, const int32_t *start_dev, uint32_t capacity, bool f16) {
   const uint32_t s0 = start_dev ? (uint32_t)*start_dev : start;
   const uint64_t total = (uint64_t)n * row;
   for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
     uint32_t t = (uint32_t)(i / row), e = (uint32_t)(i % row);
     uint64_t slot = (uint64_t)((s0 + t) % capacity) * row + e;
-    kc[slot] = k[i];
-    vc[slot] = v[i];
+    kv_put(kc, slot, k[i], f16);
+    kv_put(vc, slot, v[i], f16);
   }
 }
 
-hipError_t kv_append(hipStream_t s, const float *k, const float *v, float *kc, float *vc, uint32_t row_floats,
-                     uint32_t n, uint32_t start, const int32_t *start_dev, uint32_t capacity) {
+hipError_t kv_append(hipStream_t s, const float *k, const float *v, void *kc, void *vc, uint32_t row_floats,
+                     uint32_t n, uint32_t start, const int32_t *start_dev, uint32_t capacity, bool kv16) {
   if (!n) return hipSuccess;
   if (!capacity) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_kv_append, grid_for(n * row_floats), dim3(256), 0, s, k, v, kc, vc, row_floats, n, start,
-                     start_dev, capacity);
+                     start_dev, capacity, kv16);
+  return hipGetLastError();
+}
+
+__global__ void k_to_f16(const float *src, _Float16 *dst, uint64_t n) {
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    dst[i] = (_Float16)src[i];
+}
+
+hipError_t to_f16(hipStream_t s, const float *src, _Float16 *dst, uint64_t n) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_to_f16, grid_for(n < (1u << 30) ? (uint32_t)n : (1u << 30)), dim3(256), 0, s, src, dst, n);
   return hipGetLastError();
 }
 

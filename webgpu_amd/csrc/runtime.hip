@@ -396,30 +396,33 @@ int wgd_rope_adjacent(wgd_context *ctx, wgd_buffer *x, uint32_t heads, uint32_t 
 static int attention_args(wgd_context *ctx, const char *what, const wgd_buffer *q, const wgd_buffer *k,
                           const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                           uint32_t start, float scale, uint32_t window, uint32_t capacity, uint32_t context,
-                          uint32_t batch, AttnArgs &a) {
+                          uint32_t batch, AttnArgs &a, bool kv16 = false) {
   NEED_BUF(ctx, q, what); NEED_BUF(ctx, k, what); NEED_BUF(ctx, v, what); NEED_BUF(ctx, y, what);
+  const uint64_t esz = kv16 ? 2 : 4;  // bytes per ring element
   uint32_t cap = capacity ? capacity : context;
   if (!kv_heads || !heads || heads % kv_heads || !hd || hd > 512 || !cap || !window)
     return fail(ctx, WGD_E_INVALID, "%s: invalid heads %u/%u, head_dim %u, capacity %u or window %u", what, heads, kv_heads, hd, cap, window);
   if ((heads / kv_heads) > 16) return fail(ctx, WGD_E_INVALID, "%s: more than 16 query heads per KV head", what);
   NEED_FIT(ctx, q, (uint64_t)batch * heads * hd * 4, "attention queries");
-  NEED_FIT(ctx, k, (uint64_t)cap * kv_heads * hd * 4, "attention keys");
-  NEED_FIT(ctx, v, (uint64_t)cap * kv_heads * hd * 4, "attention values");
+  NEED_FIT(ctx, k, (uint64_t)cap * kv_heads * hd * esz, "attention keys");
+  NEED_FIT(ctx, v, (uint64_t)cap * kv_heads * hd * esz, "attention values");
   NEED_FIT(ctx, y, (uint64_t)batch * heads * hd * 4, "attention output");
   a = AttnArgs{};
-  a.q = (const float *)q->ptr; a.k = (const float *)k->ptr; a.v = (const float *)v->ptr; a.y = (float *)y->ptr;
+  a.q = (const float *)q->ptr; a.k = k->ptr; a.v = v->ptr; a.y = (float *)y->ptr;
+  a.kv16 = kv16;
   a.heads = heads; a.kv_heads = kv_heads; a.hd = hd; a.start = start; a.start_dev = nullptr;
   a.scale = scale; a.window = window; a.capacity = cap; a.batch = batch;
   a.partial = nullptr; a.partial_floats = 0;
   return WGD_OK;
 }
 
-int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, const wgd_buffer *v, wgd_buffer *y,
-                  uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t start, float scale, uint32_t window,
-                  uint32_t capacity, uint32_t context, uint32_t batch) {
+static int attention_common(wgd_context *ctx, const char *what, const wgd_buffer *q, const wgd_buffer *k,
+                            const wgd_buffer *v, wgd_buffer *y, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                            uint32_t start, float scale, uint32_t window, uint32_t capacity, uint32_t context,
+                            uint32_t batch, bool kv16) {
   NEED_CTX(ctx);
   AttnArgs a;
-  int rc = attention_args(ctx, "attention", q, k, v, y, heads, kv_heads, hd, start, scale, window, capacity, context, batch, a);
+  int rc = attention_args(ctx, what, q, k, v, y, heads, kv_heads, hd, start, scale, window, capacity, context, batch, a, kv16);
   if (rc || !batch) return rc;
   uint64_t need = attention_scratch_floats(heads, hd, batch, (uint32_t)device_cu_count() * 4);
   if (need > ctx->att_partial_floats) {
@@ -431,7 +434,33 @@ int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, co
     ctx->att_partial = (float *)p; ctx->att_partial_floats = need;
   }
   a.partial = ctx->att_partial; a.partial_floats = (uint32_t)(ctx->att_partial_floats > 0xFFFFFFFFull ? 0xFFFFFFFFull : ctx->att_partial_floats);
-  return ctx_check(ctx, attention(ctx->stream, a), "attention");
+  return ctx_check(ctx, attention(ctx->stream, a), what);
+}
+
+int wgd_attention(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, const wgd_buffer *v, wgd_buffer *y,
+                  uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t start, float scale, uint32_t window,
+                  uint32_t capacity, uint32_t context, uint32_t batch) {
+  return attention_common(ctx, "attention", q, k, v, y, heads, kv_heads, hd, start, scale, window, capacity, context,
+                          batch, false);
+}
+
+int wgd_attention_f16kv(wgd_context *ctx, const wgd_buffer *q, const wgd_buffer *k, const wgd_buffer *v,
+                        wgd_buffer *y, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t start, float scale,
+                        uint32_t window, uint32_t capacity, uint32_t context, uint32_t batch) {
+  return attention_common(ctx, "attention_f16kv", q, k, v, y, heads, kv_heads, hd, start, scale, window, capacity,
+                          context, batch, true);
+}
+
+int wgd_kv_store_f16(wgd_context *ctx, const wgd_buffer *src, wgd_buffer *dst, uint64_t count, uint64_t src_offset,
+                     uint64_t dst_offset) {
+  NEED_CTX(ctx); NEED_BUF(ctx, src, "kv_store_f16"); NEED_BUF(ctx, dst, "kv_store_f16");
+  if (src_offset > src->size / 4 || count > src->size / 4 - src_offset || dst_offset > dst->size / 2 ||
+      count > dst->size / 2 - dst_offset)
+    return fail(ctx, WGD_E_INVALID, "kv_store_f16: %llu values from float %llu of a %llu-byte buffer into half %llu of a "
+                "%llu-byte buffer overrun", (unsigned long long)count, (unsigned long long)src_offset,
+                (unsigned long long)src->size, (unsigned long long)dst_offset, (unsigned long long)dst->size);
+  return ctx_check(ctx, to_f16(ctx->stream, (const float *)src->ptr + src_offset, (_Float16 *)dst->ptr + dst_offset, count),
+                   "kv_store_f16");
 }
 
 int wgd_probe_read(wgd_context *ctx, const wgd_buffer *src, uint64_t bytes, uint32_t copies, uint32_t launches,

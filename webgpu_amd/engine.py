@@ -108,12 +108,16 @@ class ByteSource:
 class LoadOptions:
     """engine.ts:19. ``batchSize`` defaults to the performance mode's batch.
     ``gpuBudgetMiB`` caps the context's device allocations (None: no cap); the reference's
-    16 GiB ceiling is a browser limit and is not applied."""
+    16 GiB ceiling is a browser limit and is not applied. ``kvCacheType`` "f16" keeps the K/V
+    rings in half precision (values rounded to nearest even when cached, attention math in
+    f32): half the ring memory and the bytes a decode step reads. The reference's rings are
+    f32 (engine.ts:98-101), the default."""
     contextLength: int = 512
     batchSize: Optional[int] = None
     gpuBudgetMiB: Optional[int] = None
     performance: str = "low-memory"
     device: int = 0
+    kvCacheType: str = "f32"
 
 
 @dataclass
@@ -153,7 +157,7 @@ class ModelInfo:
     stats: Dict[str, Any]
 
 
-def _config_struct(c: ModelConfig, context: int, batch: int) -> ModelConfigC:
+def _config_struct(c: ModelConfig, context: int, batch: int, kv_f16: bool = False) -> ModelConfigC:
     s = ModelConfigC()
     gemma = c.family == "gemma3"
     s.family = 1 if gemma else 0
@@ -171,6 +175,7 @@ def _config_struct(c: ModelConfig, context: int, batch: int) -> ModelConfigC:
     s.epsilon, s.theta, s.local_theta = c.epsilon, c.theta, c.localTheta
     s.attention_scale, s.rope_scale = c.attentionScale, c.ropeScale
     s.embed_scale = math.sqrt(c.hidden) if c.architecture == "gemma3" else 1.0
+    s.kv_f16 = 1 if kv_f16 else 0
     return s
 
 
@@ -189,6 +194,7 @@ class PagedEngine:
         self.budget: Optional[int] = None
         self.performance = "low-memory"
         self.kvCapacities: List[int] = []
+        self.kvCacheType = "f32"
         self.busy = False
         self.disposed = False
         self.tokensInCache: List[int] = []
@@ -209,6 +215,9 @@ class PagedEngine:
         if o.gpuBudgetMiB is not None and (not isinstance(o.gpuBudgetMiB, int) or o.gpuBudgetMiB < 512):
             raise ValueError("GPU budget must be at least 512 MiB.")
         self.budget = o.gpuBudgetMiB
+        if o.kvCacheType not in ("f32", "f16"):
+            raise ValueError("KV cache type must be f32 or f16.")
+        self.kvCacheType = o.kvCacheType
         self.source = source if isinstance(source, ByteSource) else ByteSource(source)
         self.progress({"phase": "loading", "detail": "Reading GGUF metadata", "fraction": 0.05})
         self.gguf = read_gguf(self.source)
@@ -216,12 +225,12 @@ class PagedEngine:
         validate_context(self.context, c.maxContext)
         # the GGUF's tokenizer (None for a file that carries none: token-id prompts only)
         self.tokenizer = tokenizer_for(self.gguf.metadata, c.architecture, c.family)
-        memory = attention_memory(c, self.context, self.batch)
+        memory = attention_memory(c, self.context, self.batch, 2 if o.kvCacheType == "f16" else 4)
         self.kvCapacities = list(memory["capacities"])
         self.gpu = Compute(o.gpuBudgetMiB, o.device)
         try:
             self.gpu.init()
-            cfg = _config_struct(c, self.context, self.batch)
+            cfg = _config_struct(c, self.context, self.batch, o.kvCacheType == "f16")
             cfg.tied_output = 0 if "output.weight" in self.gguf.tensors else 1
             caps = (C.c_int32 * c.layers)(*self.kvCapacities)
             out = C.c_void_p()

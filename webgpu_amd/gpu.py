@@ -50,6 +50,8 @@ SIGNATURES = {
     "wgd_attention": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
     "wgd_attention_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
     "wgd_attention_noalloc_limit": (_U64, []),
+    "wgd_attention_f16kv": (C.c_int, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32, _U32]),
+    "wgd_kv_store_f16": (C.c_int, [_P, _P, _P, _U64, _U64, _U64]),
     "wgd_probe_read": (C.c_int, [_P, _P, _U64, _U32, _U32, _U32, _U32, _U32, _P, _U32]),
     "wgd_add": (C.c_int, [_P, _P, _P, _U32]),
     "wgd_silu": (C.c_int, [_P, _P, _P, _P, _U32]),
@@ -100,7 +102,8 @@ class ModelConfigC(C.Structure):
         "family", "rope_adjacent", "hidden", "intermediate", "layers", "heads", "kv_heads", "head_dim", "vocab",
         "rotary_dim", "window", "period", "qk_norm", "ffn_gate", "gelu", "bias_q", "bias_k", "bias_v",
         "bias_output", "tied_output", "context", "batch")] + [(n, C.c_float) for n in (
-        "epsilon", "theta", "local_theta", "attention_scale", "rope_scale")] + [("embed_scale", C.c_double)]
+        "epsilon", "theta", "local_theta", "attention_scale", "rope_scale")] + [("embed_scale", C.c_double),
+                                                                                  ("kv_f16", C.c_int32)]
 
 
 class Buffer:
@@ -250,6 +253,17 @@ class Compute:
         allocation (for graph capture and allocation-free callers)."""
         self.check(lib().wgd_attention_noalloc(self.ctx, q.ptr, k.ptr, v.ptr, y.ptr, heads, kv_heads, hd, start,
                                                scale, window, capacity, context, batch))
+
+    def attention_f16kv(self, q: Buffer, k: Buffer, v: Buffer, y: Buffer, heads: int, kv_heads: int, hd: int,
+                        start: int, scale: float, window: int, capacity: int, context: int, batch: int = 1) -> None:
+        """attention() over K/V rings of f16 elements (f32 arithmetic)."""
+        self.check(lib().wgd_attention_f16kv(self.ctx, q.ptr, k.ptr, v.ptr, y.ptr, heads, kv_heads, hd, start, scale,
+                                             window, capacity, context, batch))
+
+    def kv_store_f16(self, src: Buffer, dst: Buffer, count: int, src_offset: int = 0, dst_offset: int = 0) -> None:
+        """cacheKV's ring copy into an f16 ring: dst[dst_offset + i] = f16(src[src_offset + i])
+        (element offsets, round to nearest even)."""
+        self.check(lib().wgd_kv_store_f16(self.ctx, src.ptr, dst.ptr, count, src_offset, dst_offset))
 
     def probe_read(self, src: Buffer, nbytes: int, copies: int, launches: int, workgroups: int, threads: int,
                    depth: int, out: Optional[Buffer] = None, out_floats: int = 0) -> None:

@@ -20,14 +20,15 @@ export function outputLimit(requested, promptTokens, context) {
 }
 
 /** Per-layer ring capacities: Gemma local layers and sliding-window models keep the window
- * plus the rest of the current prompt batch. */
-export function attentionMemory(c, context, batch) {
+ * plus the rest of the current prompt batch. kvBytes counts K and V at `elementBytes` each
+ * (4 as the reference's f32 rings, 2 for f16 rings). */
+export function attentionMemory(c, context, batch, elementBytes = 4) {
   const capacities = [];
   for (let l = 0; l < c.layers; l++) {
     if (c.family === 'gemma3') capacities.push(l % c.period !== c.period - 1 ? Math.min(context, c.window + batch - 1) : context);
     else if (c.slidingWindow > 0) capacities.push(Math.min(context, c.slidingWindow + batch - 1));
     else capacities.push(context);
   }
-  const kvBytes = capacities.reduce((a, b) => a + b, 0) * c.kvHeads * c.headDim * 8;
+  const kvBytes = capacities.reduce((a, b) => a + b, 0) * c.kvHeads * c.headDim * 2 * elementBytes;
   return { capacities, kvBytes, stateBytes: 0, totalBytes: kvBytes };
 }

@@ -19,7 +19,7 @@ const BATCHES = [1, 8, 16, 32, 64, 128];
 export const PRESETS = { lite: 8, 'low-memory': 16, fast: 128 };
 
 /** The wgd_model_config fields for a ModelConfig (field names of include/wgd.h). */
-export function configStruct(c, context, batch, tied) {
+export function configStruct(c, context, batch, tied, kvF16 = false) {
   const gemma = c.family === 'gemma3';
   return {
     family: gemma ? 1 : 0, rope_adjacent: c.rope === 'norm' ? 1 : 0,
@@ -30,6 +30,7 @@ export function configStruct(c, context, batch, tied) {
     tied_output: tied ? 1 : 0, context, batch,
     epsilon: c.epsilon, theta: c.theta, local_theta: c.localTheta, attention_scale: c.attentionScale,
     rope_scale: c.ropeScale, embed_scale: c.architecture === 'gemma3' ? Math.sqrt(c.hidden) : 1,
+    kv_f16: kvF16 ? 1 : 0,
   };
 }
 
@@ -47,14 +48,18 @@ export class PagedEngine {
   constructor(progress) {
     this.progress = progress || (() => {});
     this.ctx = null; this.model = null; this.source = null; this.gguf = null; this.config = null;
-    this.context = 512; this.batch = 16; this.kvCapacities = [];
+    this.context = 512; this.batch = 16; this.kvCapacities = []; this.kvCacheType = 'f32';
     this.budget = null; this.performance = 'low-memory';
     this.busy = false; this.disposed = false; this.tokensInCache = [];
   }
 
   /** PagedEngine.load (engine.ts:51-114): parse, configure, upload, seal. */
   load(path, options = {}, signal) {
-    const o = Object.assign({ contextLength: 512, gpuBudgetMiB: null, performance: 'low-memory', device: 0 }, options);
+    // kvCacheType 'f16' keeps the K/V rings in half precision (rounded to nearest even when
+    // cached, attention math in f32); the reference's rings are f32 (engine.ts:98-101)
+    const o = Object.assign({ contextLength: 512, gpuBudgetMiB: null, performance: 'low-memory', device: 0, kvCacheType: 'f32' }, options);
+    if (o.kvCacheType !== 'f32' && o.kvCacheType !== 'f16') throw new Error('KV cache type must be f32 or f16.');
+    this.kvCacheType = o.kvCacheType;
     if (!(o.performance in PRESETS)) throw new Error('Performance must be lite, low-memory or fast.');
     this.performance = o.performance; this.budget = o.gpuBudgetMiB;
     this.context = o.contextLength; this.batch = o.batchSize === undefined || o.batchSize === null ? PRESETS[o.performance] : o.batchSize;
@@ -67,11 +72,12 @@ export class PagedEngine {
     this.gguf = readGGUF(this.source);
     const c = this.config = modelConfig(this.gguf);
     validateContext(this.context, c.maxContext);
-    this.kvCapacities = attentionMemory(c, this.context, this.batch).capacities;
+    this.kvCapacities = attentionMemory(c, this.context, this.batch, o.kvCacheType === 'f16' ? 2 : 4).capacities;
     this.ctx = addon.create(o.device, o.gpuBudgetMiB);
     try {
       const tied = !this.gguf.tensors.has('output.weight');
-      this.model = addon.modelCreate(this.ctx, configStruct(c, this.context, this.batch, tied), Int32Array.from(this.kvCapacities));
+      this.model = addon.modelCreate(this.ctx, configStruct(c, this.context, this.batch, tied, o.kvCacheType === 'f16'),
+        Int32Array.from(this.kvCapacities));
       const tensors = [...this.gguf.tensors.values()].filter((t) => (t.dims.length === 1 || t.dims.length === 2) &&
         (!t.name.startsWith('blk.') || Number(t.name.split('.')[1]) < c.layers));
       tensors.forEach((t, i) => {

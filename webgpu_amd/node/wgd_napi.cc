@@ -195,6 +195,11 @@ napi_value model_create(napi_env env, napi_callback_info info) {
     *f.p = (float)d;
   }
   if (!field_f64(env, argv[1], "embed_scale", &cfg.embed_scale)) return throw_msg(env, "WGD_E_INVALID", "config.embed_scale must be a number");
+  // kv_f16 is optional (absent: the reference's f32 rings)
+  bool has_kv = false;
+  if (napi_has_named_property(env, argv[1], "kv_f16", &has_kv) == napi_ok && has_kv &&
+      !field_i32(env, argv[1], "kv_f16", &cfg.kv_f16))
+    return throw_msg(env, "WGD_E_INVALID", "config.kv_f16 must be a number");
   void *caps = nullptr;
   size_t n = 0;
   if (!typed(env, argv[2], napi_int32_array, &caps, &n) || (int32_t)n != cfg.layers)
@@ -632,9 +637,9 @@ napi_value rope_plain(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
-// attention / attentionNoalloc(ctx, q, k, v, y, heads, kvHeads, headDim, start, scale,
-// window, capacity, context, batch)
-template <int NOALLOC>
+// attention / attentionNoalloc / attentionF16kv(ctx, q, k, v, y, heads, kvHeads, headDim,
+// start, scale, window, capacity, context, batch)
+template <int KIND>
 napi_value attention(napi_env env, napi_callback_info info) {
   ARGS(14);
   CTX_ARG();
@@ -651,10 +656,26 @@ napi_value attention(napi_env env, napi_callback_info info) {
   U32_ARG(11, capacity);
   U32_ARG(12, context);
   U32_ARG(13, batch);
-  if (NOALLOC)
+  if (KIND == 1)
     CHECK(c->ctx, wgd_attention_noalloc(c->ctx, q, k, v, y, heads, kvHeads, hd, start, (float)scale, window, capacity, context, batch));
+  else if (KIND == 2)
+    CHECK(c->ctx, wgd_attention_f16kv(c->ctx, q, k, v, y, heads, kvHeads, hd, start, (float)scale, window, capacity, context, batch));
   else
     CHECK(c->ctx, wgd_attention(c->ctx, q, k, v, y, heads, kvHeads, hd, start, (float)scale, window, capacity, context, batch));
+  return undefined(env);
+}
+
+// kvStoreF16(ctx, src, dst, count, srcOffset, dstOffset): cacheKV's copy into an f16 ring
+// (element offsets)
+napi_value kv_store_f16(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  CTX_ARG();
+  BUF_ARG(1, src);
+  BUF_ARG(2, dst);
+  U64_ARG(3, count);
+  U64_ARG(4, so);
+  U64_ARG(5, dof);
+  CHECK(c->ctx, wgd_kv_store_f16(c->ctx, src, dst, count, so, dof));
   return undefined(env);
 }
 
@@ -764,6 +785,7 @@ napi_value init(napi_env env, napi_value exports) {
       {"matmul", matmul}, {"quantizedBytes", quantized_bytes}, {"quantize", quantize}, {"matvec", matvec},
       {"dequant", dequant}, {"norm", norm}, {"ropeNorm", rope_norm}, {"ropeNeox", rope_plain<0>},
       {"ropeAdjacent", rope_plain<1>}, {"attention", attention<0>}, {"attentionNoalloc", attention<1>},
+      {"attentionF16kv", attention<2>}, {"kvStoreF16", kv_store_f16},
       {"add", add}, {"silu", glu<0>}, {"gelu", glu<1>}, {"biasAdd", bias_add}, {"activate", activate},
       {"argmax", argmax}, {"sample", sample}, {"embed", embed}};
   for (auto &f : fns) {
