@@ -265,6 +265,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=None, help="timed decode tokens (default: per model)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: per model)")
+    ap.add_argument("--kv", default="f32", choices=["f32", "f16"],
+                    help="K/V ring element type (f32 as the reference; f16 halves the ring bytes)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-matvec", action="store_true", help="skip the matvec microbench")
     ap.add_argument("--matvec-only", action="store_true",
@@ -351,7 +353,7 @@ def main() -> None:
           file=sys.stderr, flush=True)
     eng = PagedEngine()
     t = time.perf_counter()
-    eng.load(f, LoadOptions(contextLength=context, batchSize=128))
+    eng.load(f, LoadOptions(contextLength=context, batchSize=128, kvCacheType=a.kv))
     print(f"[bench] loaded in {time.perf_counter() - t:.1f} s on {eng.gpu.adapterName}", file=sys.stderr, flush=True)
     ids = synth.prompt_ids(eng.config.vocab, a.prompt, seed=7)
 
@@ -374,10 +376,12 @@ def main() -> None:
     print(f"[bench] prefill {a.prompt} tokens in {prefill_s * 1e3:.1f} ms (median of 3 after a warm-up pass)",
           file=sys.stderr, flush=True)
 
+    # warm-up steps run over the first positions after the prompt, then the timed steps decode
+    # the same positions again (rewriting the same ring slots), so the timed window is the
+    # workload's span [prompt, prompt + steps) whatever the warm-up count
     pos = a.prompt
     if a.warmup:
-        warm = eng.decode(token, pos, a.warmup)
-        token, pos = warm[-1], pos + a.warmup
+        eng.decode(token, pos, a.warmup)
     eng.gpu.done()
     t0 = time.perf_counter()
     toks = eng.decode(token, pos, a.steps)
@@ -398,16 +402,38 @@ def main() -> None:
     eng.set_sampling(0.0)
     print(f"[bench] decode with sampling (T 0.7, top-k 40, top-p 0.9): {sampled:.1f} tok/s", file=sys.stderr, flush=True)
 
+    # decode attention alone (one layer's launch pair, HIP events), at the middle and the end
+    # of the timed window; Gemma-3 at a local (sliding) and a global layer. Bytes: the K and V
+    # rows of every attended key (min(pos + 1, window) keys x kv_heads x head_dim x 2).
+    attn = []
+    esz = 2 if a.kv == "f16" else 4
+    cfg = eng.config
+    gemma = cfg.family == "gemma3"
+    layers = [0, cfg.period - 1] if gemma else [0]
+    for layer in layers:
+        window = cfg.window if gemma and layer % cfg.period != cfg.period - 1 else context
+        for p in sorted({pos + a.steps // 2, pos + a.steps}):
+            if p >= context:
+                continue
+            us = eng.attention_timing(layer, p, 50)
+            nbytes = min(p + 1, window) * spec.kv_heads * spec.head_dim * 2 * esz
+            attn.append({"layer": layer, "pos": p, "keys": min(p + 1, window), "us": us, "bytes": nbytes,
+                         "GBps": nbytes / us / 1e3, "frac": nbytes / us / 1e3 / (PEAK_HBM / 1e9)})
+            print(f"[bench] decode attention layer {layer} at position {p}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s "
+                  f"({100 * nbytes / us / 1e3 / (PEAK_HBM / 1e9):.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+
     result = {
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": dt * 1e3 / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "decode_sampled_tok_s": sampled,
         "dtype": "f32", "data": "synthetic (seeded random-init Q4_K_M GGUF)",
         "config": {"workload": f"{a.model}-shape Q4_K_M greedy decode", "prompt": a.prompt, "prefill_batch": 128,
-                   "decode_tokens": a.steps, "context": context, "kv_cache": "f32",
+                   "decode_tokens": a.steps, "context": context, "kv_cache": a.kv,
                    "layers": spec.layers, "hidden": spec.hidden, "heads": spec.heads, "kv_heads": spec.kv_heads,
                    "ffn": spec.ffn, "vocab": spec.vocab},
         "prefill_tok_s": a.prompt / prefill_s,
+        "decode_window": [pos, pos + a.steps],
+        "attention": attn,
     }
     eng.dispose()
 

@@ -267,6 +267,14 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count,
  * Validated as the reference validates GenerationOptions (WGD_E_INVALID). */
 int wgd_model_sampling(wgd_model *m, double temperature, uint32_t top_k, double top_p, uint64_t seed);
 void wgd_model_destroy(wgd_model *m);
+/* Measurement, no reference counterpart: the mean device time in microseconds (HIP events
+ * on the context's stream) of `reps` back-to-back launches of the decode step's attention
+ * of `layer` at position `pos` (Q/K norm and RoPE of the token, its K/V written to ring slot
+ * pos % capacity, split-K attention over the keys before it, merge and quantization for the
+ * O projection), on the token's current q/k/v work buffers. It overwrites that ring slot, so
+ * call it where the slot holds no live key. Models whose decode step has no fused attention
+ * launch return WGD_E_INVALID. */
+int wgd_model_attention_timing(wgd_model *m, int32_t layer, int32_t pos, int32_t reps, double *us);
 
 #ifdef __cplusplus
 }

@@ -60,8 +60,9 @@ def test_addon_exports_engine_surface():
     assert json.loads(r.stdout) == sorted(NODE_EXPORTS)
 
 
-# One binding per C-ABI entry point of include/wgd.h (wgd_probe_read, a measurement
-# helper, and the wgd_last_error/size getters folded into thrown errors aside).
+# One binding per C-ABI entry point of include/wgd.h (the measurement helpers
+# wgd_probe_read and wgd_model_attention_timing, and the wgd_last_error/size getters folded
+# into thrown errors aside).
 NODE_EXPORTS = ["create", "destroy", "adapterName", "memory", "done", "modelCreate", "modelTensor", "modelReady",
                 "modelForward", "modelDecode", "modelSampling", "modelDestroy", "bufferCreate", "bufferDestroy",
                 "bufferSize", "uploadWeights", "write", "read", "copy", "clear", "matmul", "quantizedBytes",

@@ -892,6 +892,35 @@ int wgd_model_decode(wgd_model *m, int32_t token, int32_t start, int32_t count, 
   return WGD_OK;
 }
 
+int wgd_model_attention_timing(wgd_model *m, int32_t layer, int32_t pos, int32_t reps, double *us) {
+  if (!m || !us) return fail(m ? m->ctx : nullptr, WGD_E_INVALID, "wgd_model_attention_timing: NULL argument");
+  wgd_context *ctx = m->ctx;
+  hipSetDevice(ctx->device);
+  if (!m->ready) return fail(ctx, WGD_E_STATE, "Load a model first.");
+  if (!m->qpath || !m->fused_attention)
+    return fail(ctx, WGD_E_INVALID, "attention_timing: this model's decode step has no fused attention launch");
+  if (layer < 0 || layer >= m->c.layers || pos < 0 || pos >= m->c.context || reps < 1 || reps > 100000)
+    return fail(ctx, WGD_E_INVALID, "attention_timing: layer %d, position %d, %d repetitions", layer, pos, reps);
+  hipStream_t s = ctx->stream;
+  StepState st = {pos, 0, 0, 0};
+  int rc = ctx_check(ctx, hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s), "attention_timing");
+  const QXOut qx = qx_view(m->qx_o, (uint32_t)(m->c.heads * m->c.head_dim));
+  if (!rc) rc = ctx_check(ctx, decode_attention_layer(m, layer, qx), "attention_timing");  // warm
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (!rc) rc = ctx_check(ctx, hipEventCreate(&e0), "attention_timing");
+  if (!rc) rc = ctx_check(ctx, hipEventCreate(&e1), "attention_timing");
+  if (!rc) rc = ctx_check(ctx, hipEventRecord(e0, s), "attention_timing");
+  for (int32_t i = 0; !rc && i < reps; i++) rc = ctx_check(ctx, decode_attention_layer(m, layer, qx), "attention_timing");
+  if (!rc) rc = ctx_check(ctx, hipEventRecord(e1, s), "attention_timing");
+  if (!rc) rc = ctx_sync(ctx, "GPU fault during attention timing");
+  float ms = 0.f;
+  if (!rc) rc = ctx_check(ctx, hipEventElapsedTime(&ms, e0, e1), "attention_timing");
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  if (!rc) *us = (double)ms * 1e3 / reps;
+  return rc;
+}
+
 int wgd_model_sampling(wgd_model *m, double temperature, uint32_t top_k, double top_p, uint64_t seed) {
   if (!m) return fail(nullptr, WGD_E_INVALID, "wgd_model_sampling: NULL model");
   wgd_context *ctx = m->ctx;

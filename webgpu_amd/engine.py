@@ -281,6 +281,13 @@ class PagedEngine:
         self.gpu.check(lib().wgd_model_sampling(self.model, float(temperature), int(top_k), float(top_p),
                                                 int(seed) & (2 ** 64 - 1)))
 
+    def attention_timing(self, layer: int, pos: int, reps: int = 50) -> float:
+        """Measurement: mean device microseconds of the decode step's attention launch of
+        `layer` at position `pos` (it overwrites ring slot pos % capacity)."""
+        us = C.c_double(0.0)
+        self.gpu.check(lib().wgd_model_attention_timing(self.model, int(layer), int(pos), int(reps), C.byref(us)))
+        return us.value
+
     def forward_argmax(self, ids: Sequence[int], start: int) -> int:
         """forward + the token pick (greedy, or sampled: set_sampling) on the device."""
         n = len(ids)

@@ -60,6 +60,7 @@ SIGNATURES = {
     "wgd_activate": (C.c_int, [_P, _P, _U32]),
     "wgd_argmax": (C.c_int, [_P, _P, _U32, _P, C.POINTER(_I32)]),
     "wgd_sample": (C.c_int, [_P, _P, _U32, C.c_double, _U32, C.c_double, C.c_uint64, _U32, C.POINTER(_I32)]),
+    "wgd_model_attention_timing": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
     "wgd_model_sampling": (C.c_int, [_P, C.c_double, _U32, C.c_double, C.c_uint64]),
     "wgd_embed": (C.c_int, [_P, _I32, _P, _P, _P, _U32, _U32, _D]),
     "wgd_model_create": (C.c_int, [_P, _P, C.POINTER(_I32), C.POINTER(_P)]),
