@@ -207,14 +207,51 @@ hipError_t norm_add(hipStream_t s, const float *delta, const float *w, float *st
   return hipGetLastError();
 }
 
+// One row (the decode token) over many workgroups: every workgroup forms the sum of squares
+// of the whole delta row itself (its loads all go out at once: raw buffer loads, zero past
+// the row), then updates its own 256 elements of the state and writes their QX form. No
+// workgroup waits on another, and no CU streams the row alone.
+constexpr uint32_t NAW_E = 64;  // delta elements per thread: rows up to 16384
+template <uint32_t E>
+__global__ __launch_bounds__(256) void k_norm_add_qw(const float *d, const float *w, float *state, uint32_t n,
+                                                     float eps, const float *next_w, QXOut q) {
+  __shared__ float red[4];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t i = blockIdx.x * 256 + tid;
+  const bool live = i < n;
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(d), 0, (int)(4 * n), 0x00020000);
+  float dv[E];
+#pragma unroll
+  for (uint32_t e = 0; e < E; e++)
+    dv[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rd, 4 * (tid + 256 * e), 0, 0));
+  const float sv = live ? state[i] : 0.f, ww = live ? w[i] : 0.f, nw = live ? next_w[i] : 0.f;
+  const float mine = live ? d[i] : 0.f;
+  float s = 0.f;
+#pragma unroll
+  for (uint32_t e = 0; e < E; e++) s += dv[e] * dv[e];
+  s = wave_sum(s);
+  if (lane == 0) red[wv] = s;
+  __syncthreads();
+  s = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.f / sqrtf(s / (float)n + eps);
+  const float nv = live ? sv + mine * inv * ww : 0.f;
+  if (live) state[i] = nv;
+  qx_store(q, i, live ? nv * nw : 0.f, nv, live);
+}
+
 hipError_t norm_add_quantize(hipStream_t s, const float *delta, const float *w, float *state, uint32_t n, float eps,
                              const float *next_w, const QXOut &q) {
   if (!n || n % 16 || !next_w) return hipErrorInvalidValue;
-  if (n > NA_T * NA_E) {
+  if (n > 256 * NAW_E) {
     WGD_HIP(norm_add(s, delta, w, state, n, eps, 1));
     return quantize(s, state, n, next_w, q);
   }
-  hipLaunchKernelGGL(k_norm_add_q, dim3(1), dim3(NA_T), 0, s, delta, w, state, n, eps, next_w, q);
+  const dim3 grid((n + 255) / 256);
+  const uint32_t per = (n + 255) / 256;  // delta elements per thread
+  if (per <= 8) hipLaunchKernelGGL(k_norm_add_qw<8>, grid, dim3(256), 0, s, delta, w, state, n, eps, next_w, q);
+  else if (per <= 16) hipLaunchKernelGGL(k_norm_add_qw<16>, grid, dim3(256), 0, s, delta, w, state, n, eps, next_w, q);
+  else if (per <= 32) hipLaunchKernelGGL(k_norm_add_qw<32>, grid, dim3(256), 0, s, delta, w, state, n, eps, next_w, q);
+  else hipLaunchKernelGGL(k_norm_add_qw<NAW_E>, grid, dim3(256), 0, s, delta, w, state, n, eps, next_w, q);
   return hipGetLastError();
 }
 
