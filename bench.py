@@ -265,6 +265,11 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=None, help="timed decode tokens (default: per model)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: per model)")
+    ap.add_argument("--eager", action="store_true",
+                    help="decode with one forward per token (eager launches, host round trip per token) instead of "
+                         "graph replays: for kernel traces, whose profiler does not follow graph launches; the "
+                         "tok/s of such a run is not the metric")
+    ap.add_argument("--no-attention-timing", action="store_true", help="skip the decode attention timing")
     ap.add_argument("--kv", default="f32", choices=["f32", "f16"],
                     help="K/V ring element type (f32 as the reference; f16 halves the ring bytes)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -380,11 +385,20 @@ def main() -> None:
     # the same positions again (rewriting the same ring slots), so the timed window is the
     # workload's span [prompt, prompt + steps) whatever the warm-up count
     pos = a.prompt
+
+    def decode(n):
+        if not a.eager:
+            return eng.decode(token, pos, n)
+        out, t = [], token
+        for i in range(n):
+            t = eng.forward_argmax([t], pos + i)
+            out.append(t)
+        return out
     if a.warmup:
-        eng.decode(token, pos, a.warmup)
+        decode(a.warmup)
     eng.gpu.done()
     t0 = time.perf_counter()
-    toks = eng.decode(token, pos, a.steps)
+    toks = decode(a.steps)
     eng.gpu.done()
     dt = time.perf_counter() - t0
     value = a.steps / dt
@@ -392,15 +406,18 @@ def main() -> None:
 
     # the same decode with the reference's default sampling (reported, not the metric): the
     # same positions again, each step drawing on the device (its own decode graph)
-    eng.set_sampling(0.7, 40, 0.9, seed=1)
-    eng.decode(token, pos, 2)
-    eng.gpu.done()
-    t0 = time.perf_counter()
-    eng.decode(token, pos, a.steps)
-    eng.gpu.done()
-    sampled = a.steps / (time.perf_counter() - t0)
-    eng.set_sampling(0.0)
-    print(f"[bench] decode with sampling (T 0.7, top-k 40, top-p 0.9): {sampled:.1f} tok/s", file=sys.stderr, flush=True)
+    sampled = None
+    if not a.eager:
+        eng.set_sampling(0.7, 40, 0.9, seed=1)
+        eng.decode(token, pos, 2)
+        eng.gpu.done()
+        t0 = time.perf_counter()
+        eng.decode(token, pos, a.steps)
+        eng.gpu.done()
+        sampled = a.steps / (time.perf_counter() - t0)
+        eng.set_sampling(0.0)
+        print(f"[bench] decode with sampling (T 0.7, top-k 40, top-p 0.9): {sampled:.1f} tok/s", file=sys.stderr,
+              flush=True)
 
     # decode attention alone (one layer's launch pair, HIP events), at the middle and the end
     # of the timed window; Gemma-3 at a local (sliding) and a global layer. Bytes: the K and V
@@ -410,7 +427,7 @@ def main() -> None:
     cfg = eng.config
     gemma = cfg.family == "gemma3"
     layers = [0, cfg.period - 1] if gemma else [0]
-    for layer in layers:
+    for layer in [] if a.no_attention_timing else layers:
         window = cfg.window if gemma and layer % cfg.period != cfg.period - 1 else context
         for p in sorted({pos + a.steps // 2, pos + a.steps}):
             if p >= context:

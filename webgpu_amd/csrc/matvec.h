@@ -141,6 +141,13 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
 // (store, residual add, or act(W x) * (W1 x) for a gated pair). `out` re-quantizes the
 // result of a single-target launch.
 hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int epi, const MVOut *out = nullptr);
+// Measures the launch shapes of one launch signature on `nsets` target sets of n segments
+// each (sets[k * n .. k * n + n), e.g. one per layer) and keeps the fastest for later mv()
+// calls with that signature. Every candidate computes the same bits. The launches write
+// their outputs as mv() would (residual adds repeat), so call it before the buffers hold
+// state. Signatures already measured, F16 matrices and argmax-key launches are left alone.
+hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t n, const QXView &x, int epi,
+                   const MVOut *out = nullptr);
 inline hipError_t mv(hipStream_t s, const Matrix &w, const Matrix *w1, const QXView &x, float *y, int epi,
                      const MVOut *out = nullptr) {
   MVTarget t; t.w = &w; t.w1 = w1; t.y = y;

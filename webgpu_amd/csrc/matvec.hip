@@ -29,8 +29,12 @@
 // workgroups inside a launch: on MI355X each XCD has its own L2, and device-scope fences
 // write back and invalidate it.
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "internal.h"
 #include "decode.h"
@@ -788,7 +792,98 @@ static hipError_t launch_t(hipStream_t s, const MV &m, const MVPlan &p) {
   return hipErrorInvalidValue;
 }
 
+// Launch shapes measured by mv_tune, per device and launch signature (weight types, K, the
+// segments' rows, gated pair, epilogue, re-quantized output).
+namespace {
+typedef std::tuple<int, int, int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, bool, int, bool> PlanKey;
+std::mutex g_plan_mu;
+std::map<PlanKey, MVPlan> g_plans;
+
+PlanKey plan_key(const MVTarget *t, uint32_t n, int epi, bool qout) {
+  int t1 = t[0].w->type;
+  for (uint32_t i = 0; i < n; i++)
+    if (t[i].w->type != t[0].w->type) t1 = t[i].w->type;
+  int dev = 0;
+  hipGetDevice(&dev);
+  return PlanKey(dev, t[0].w->type, t1, t[0].w->cols, n, t[0].w->rows, n > 1 ? t[1].w->rows : 0, n > 2 ? t[2].w->rows : 0,
+                 t[0].w1 != nullptr, epi, qout);
+}
+}  // namespace
+
+static hipError_t mv_launch(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int epi, const MVOut *out,
+                            const MVPlan *forced);
+
 hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int epi, const MVOut *out) {
+  return mv_launch(s, t, n, x, epi, out, nullptr);
+}
+
+// Candidates keep the cost model's K split (NS slices of NSB units, so the staged activation
+// and the order in which every row's products are summed do not change: all candidates give
+// the same bits) and vary the rows per workgroup (NR groups of ITER steps) and the pipeline
+// depth DU. Each is timed with HIP events over back-to-back launches that rotate through the
+// sets (so the weights come from HBM, not a cache); the fastest is kept for the signature.
+hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t n, const QXView &x, int epi,
+                   const MVOut *out) {
+  if (!nsets || n < 1 || n > (uint32_t)MV_MAX_SEGS) return hipErrorInvalidValue;
+  const Matrix &w0 = *sets[0].w;
+  if (w0.type == F16 || (out && out->arg_part)) return hipSuccess;  // F16 and the head keep the model's plan
+  const bool glu = sets[0].w1 != nullptr, qout = out && out->q.d0;
+  const PlanKey key = plan_key(sets, n, epi, qout);
+  {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    if (g_plans.count(key)) return hipSuccess;
+  }
+  uint32_t rows[MV_MAX_SEGS];
+  for (uint32_t i = 0; i < n; i++) rows[i] = sets[i].w->rows;
+  const MVPlan base = mv_plan(w0, rows, n, glu, qout);
+  if (!base.RT) return hipErrorInvalidValue;
+  const uint32_t ke = base.NS * base.NSB * 8 * chunk_elems(w0.type);
+  std::vector<MVPlan> cands{base};
+  for (uint32_t nr = 1; nr * base.NS <= 16; nr++)
+    for (uint32_t it = 1; it <= 8; it++) {
+      const uint32_t rt = 16 * nr * it;
+      if (rt > 64 * nr * base.NS || rt > 1024) break;
+      const uint32_t lds = lds_map(ke, base.NS, rt, glu).bytes;
+      if (lds > lds_limit()) break;
+      uint32_t tiles = 0;
+      for (uint32_t i = 0; i < n; i++) tiles += (rows[i] + rt - 1) / rt;
+      if (tiles > 4096) continue;
+      for (uint32_t du : {1u, 2u, 4u}) {
+        if (base.NSB % du || (glu && du > 2)) continue;
+        MVPlan p = base;
+        p.NR = nr; p.ITER = it; p.DU = du; p.RT = rt; p.tiles = tiles; p.threads = 64 * nr * base.NS; p.lds = lds;
+        if (p.NR != base.NR || p.ITER != base.ITER || p.DU != base.DU) cands.push_back(p);
+      }
+    }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  WGD_HIP(hipEventCreate(&e0));
+  hipError_t err = hipEventCreate(&e1);
+  MVPlan best = base;
+  double best_us = 1e30;
+  const uint32_t reps = nsets < 8 ? 16 : 2 * nsets;
+  for (const MVPlan &p : cands) {
+    if (err != hipSuccess) break;
+    for (uint32_t i = 0; i < 2 && err == hipSuccess; i++) err = mv_launch(s, sets + n * (i % nsets), n, x, epi, out, &p);
+    if (err == hipSuccess) err = hipEventRecord(e0, s);
+    for (uint32_t i = 0; i < reps && err == hipSuccess; i++) err = mv_launch(s, sets + n * (i % nsets), n, x, epi, out, &p);
+    if (err == hipSuccess) err = hipEventRecord(e1, s);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    float ms = 0.f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+    // a candidate must beat the cost model's plan by more than timing noise
+    const double us = (double)ms * 1e3 / reps * (&p == &cands[0] ? 0.98 : 1.0);
+    if (err == hipSuccess && us < best_us) { best_us = us; best = p; }
+  }
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  if (err != hipSuccess) return err;
+  std::lock_guard<std::mutex> lock(g_plan_mu);
+  g_plans[key] = best;
+  return hipSuccess;
+}
+
+static hipError_t mv_launch(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int epi, const MVOut *out,
+                            const MVPlan *forced) {
   if (n < 1 || n > (uint32_t)MV_MAX_SEGS) return hipErrorInvalidValue;
   const Matrix &w0 = *t[0].w;
   const bool glu = t[0].w1 != nullptr;
@@ -848,7 +943,15 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
     }
     rows[i] = w.rows;
   }
-  const MVPlan p = mv_plan(w0, rows, n, glu, qout);
+  MVPlan p{};
+  if (forced) {
+    p = *forced;
+  } else {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    const auto it = g_plans.find(plan_key(t, n, epi, qout));
+    if (it != g_plans.end()) p = it->second;
+  }
+  if (!p.RT) p = mv_plan(w0, rows, n, glu, qout);
   if (!p.RT || p.threads != 64 * p.NS * p.NR || p.threads > 1024 || p.RT > p.threads || p.NSB % p.DU ||
       p.lds > lds_limit() || (qout && p.RT % 16))
     return hipErrorInvalidValue;

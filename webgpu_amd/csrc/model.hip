@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <utility>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -381,22 +382,96 @@ QXView qv(void *p, uint32_t K, bool normed = false, float eps = 0.f) { return qx
 
 // Matvecs of several matrices that read the same activation: one launch per group of at
 // most two types that mix (Q6_K with Q4_K or Q5_K), else one per weight type.
-hipError_t mv_group(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x) {
+std::vector<std::vector<MVTarget>> mv_groups(const MVTarget *t, uint32_t n) {
+  std::vector<std::vector<MVTarget>> out;
   bool done[MV_MAX_SEGS] = {};
   for (uint32_t i = 0; i < n; i++) {
     if (done[i]) continue;
-    MVTarget grp[MV_MAX_SEGS];
-    uint32_t k = 0;
+    std::vector<MVTarget> grp;
     const int a = t[i].w->type;
     int b = a;
     for (uint32_t j = i; j < n; j++) {
       const int ty = t[j].w->type;
       if (done[j]) continue;
       if (ty != a && b == a && mv_mixable(a, ty)) b = ty;
-      if (ty == a || ty == b) { grp[k++] = t[j]; done[j] = true; }
+      if (ty == a || ty == b) { grp.push_back(t[j]); done[j] = true; }
     }
-    WGD_HIP(mv(s, grp, k, x, MV_STORE));
+    out.push_back(grp);
   }
+  return out;
+}
+hipError_t mv_group(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x) {
+  for (const auto &grp : mv_groups(t, n)) WGD_HIP(mv(s, grp.data(), (uint32_t)grp.size(), x, MV_STORE));
+  return hipSuccess;
+}
+
+// The decode step's matvec launch shapes, measured on this model's weights before any state
+// lives in the buffers the launches write (mv_tune: every candidate computes the same bits).
+// The launches are the ones decode_step_q makes, grouped by weight-type signature, each
+// timed over the layers that share it.
+hipError_t tune_decode(wgd_model *m) {
+  const wgd_model_config &c = m->c;
+  hipStream_t s = m->ctx->stream;
+  const uint32_t H = c.hidden, qd = c.heads * c.head_dim, F = c.intermediate;
+  const bool gemma = is_gemma(m);
+  typedef std::vector<int> Sig;
+  auto sig_of = [](const std::vector<MVTarget> &g) {
+    Sig k;
+    for (const MVTarget &t : g) { k.push_back(t.w->type); k.push_back((int)t.w->rows); k.push_back(t.w1 ? 1 : 0); }
+    return k;
+  };
+  // Q, K and V of the normed input
+  {
+    std::map<Sig, std::vector<MVTarget>> sets;
+    std::map<Sig, uint32_t> width;
+    for (int l = 0; l < c.layers; l++) {
+      const Layer &L = m->L[l];
+      MVTarget qkv[3];
+      qkv[0].w = &L.q; qkv[0].y = m->q; qkv[0].bias = L.bq;
+      qkv[1].w = &L.k; qkv[1].y = m->k; qkv[1].bias = L.bk;
+      qkv[2].w = &L.v; qkv[2].y = m->v; qkv[2].bias = L.bv;
+      for (const auto &g : mv_groups(qkv, 3)) {
+        const Sig k = sig_of(g);
+        sets[k].insert(sets[k].end(), g.begin(), g.end());
+        width[k] = (uint32_t)g.size();
+      }
+    }
+    for (const auto &kv : sets)
+      WGD_HIP(mv_tune(s, kv.second.data(), (uint32_t)(kv.second.size() / width[kv.first]), width[kv.first],
+                      qv(m->qx_attn, H, true, c.epsilon), MV_STORE));
+  }
+  // O (into the residual, re-quantized with ffn_norm; Gemma: stored for the post-norm), the
+  // gated gate/up pair, and down
+  MVOut to_ffn;
+  to_ffn.q = qx_view(m->qx_ffn, H); to_ffn.norm_w = m->L[0].ffn_norm;
+  MVOut to_down;
+  to_down.q = qx_view(m->qx_down, F);
+  MVOut next;
+  next.q = qx_view(m->qx_attn, H); next.norm_w = m->L[0].attn_norm;
+  std::map<Sig, std::vector<MVTarget>> o_sets, gu_sets, dn_sets;
+  for (int l = 0; l < c.layers; l++) {
+    const Layer &L = m->L[l];
+    MVTarget o;
+    o.w = &L.o; o.bias = L.bo; o.y = gemma ? m->proj : m->hidden;
+    o_sets[sig_of({o})].push_back(o);
+    if (c.ffn_gate) {
+      MVTarget gu;
+      gu.w = &L.gate; gu.w1 = &L.up; gu.y = m->prod;
+      gu_sets[sig_of({gu})].push_back(gu);
+    }
+    MVTarget dn;
+    dn.w = &L.down; dn.y = gemma ? m->down : m->hidden;
+    dn_sets[sig_of({dn})].push_back(dn);
+  }
+  for (const auto &kv : o_sets)
+    WGD_HIP(mv_tune(s, kv.second.data(), (uint32_t)kv.second.size(), 1, qv(m->qx_o, qd), gemma ? MV_STORE : MV_ADD,
+                    gemma ? nullptr : &to_ffn));
+  for (const auto &kv : gu_sets)
+    WGD_HIP(mv_tune(s, kv.second.data(), (uint32_t)kv.second.size(), 1, qv(m->qx_ffn, H, true, c.epsilon),
+                    c.gelu ? MV_GELU : MV_SILU, &to_down));
+  for (const auto &kv : dn_sets)
+    WGD_HIP(mv_tune(s, kv.second.data(), (uint32_t)kv.second.size(), 1, qv(m->qx_down, F), gemma ? MV_STORE : MV_ADD,
+                    gemma ? nullptr : &next));
   return hipSuccess;
 }
 
@@ -793,6 +868,8 @@ int wgd_model_ready(wgd_model *m) {
       }
       if (rc) return rc;
     }
+    rc = ctx_check(ctx, tune_decode(m), "decode launch shapes");
+    if (rc) return rc;
   }
   m->ready = true;
   return ctx_sync(ctx, "model upload");
