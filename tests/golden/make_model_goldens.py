@@ -14,7 +14,14 @@ under any implementation that meets that tolerance. So prompt seeds are tried in
 from 7, a seed is dropped at its first such step, and the fixture keeps the first seed
 whose every step clears the tolerance, with the dropped seeds listed.
 
-    python tests/golden/make_model_goldens.py [name ...]
+At the 8B shape one oracle attempt costs 10-20 minutes and most seeds meet a step inside
+the tolerance within 256 tokens (seeds 7-10 did, at steps 52, 30, 85 and 250). Its prompt
+seeds were therefore screened first on the device (the engine's own logits, every step's
+top-2 margin at least 1.15e-3 of max|logit| over the 512 + 256 tokens; 5 of seeds 11-1499
+passed: 236, 613, 739, 864, 1321), and the oracle then confirms the screened seeds given
+with --seeds, in order: the fixture is still the oracle's tokens and margins.
+
+    python tests/golden/make_model_goldens.py [name ...] [--seeds 613,739]
 """
 import os
 import sys
@@ -77,7 +84,7 @@ def run(ora, c, name: str, pseed: int, prompt_len: int, steps: int, t0: float):
     return ids, toks, margins, maxabs, first_logits, logits.astype(np.float32)
 
 
-def make(name: str) -> str:
+def make(name: str, seeds=None) -> str:
     prompt_len, steps, context = WORKLOADS[name]
     t0 = time.time()
     f = synth.build(name)
@@ -86,7 +93,7 @@ def make(name: str) -> str:
     caps = attention_memory(c, context, CHUNK)["capacities"]
     rejected = []
     got = None
-    for pseed in range(FIRST_SEED, FIRST_SEED + MAX_SEEDS):
+    for pseed in seeds or range(FIRST_SEED, FIRST_SEED + MAX_SEEDS):
         # a fresh oracle per seed: its rings start empty, as a freshly loaded engine's do
         ora = orc.OracleModel(f, g, c, context, caps)
         try:
@@ -111,5 +118,11 @@ def make(name: str) -> str:
 
 
 if __name__ == "__main__":
-    for n in sys.argv[1:] or list(WORKLOADS):
-        make(n)
+    args = sys.argv[1:]
+    seeds = None
+    if "--seeds" in args:
+        i = args.index("--seeds")
+        seeds = [int(v) for v in args[i + 1].split(",")]
+        del args[i:i + 2]
+    for n in args or list(WORKLOADS):
+        make(n, seeds)

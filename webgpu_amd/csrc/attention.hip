@@ -640,7 +640,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnDecK a) {
 // f64 as in k_rope); the workgroup whose chunk holds the position writes the new key and
 // value into the ring (slot pos % capacity: the ring keeps at least the window, so no
 // other chunk of this launch reads it) and uses the fresh values for that key.
-constexpr uint32_t AD2_DB = 4;  // key iterations (KPW keys each) per wavefront load batch
+constexpr uint32_t AD2_DB = 2;  // key iterations (KPW keys each) per wavefront load batch
 
 template <uint32_t LPK>
 __device__ __forceinline__ float group_sum(float v) {
