@@ -396,6 +396,8 @@ std::vector<std::vector<MVTarget>> mv_groups(const MVTarget *t, uint32_t n) {
       if (ty != a && b == a && mv_mixable(a, ty)) b = ty;
       if (ty == a || ty == b) { grp.push_back(t[j]); done[j] = true; }
     }
+    // the heavier Q6_K segments first: their workgroups dispatch first
+    std::stable_partition(grp.begin(), grp.end(), [](const MVTarget &t) { return t.w->type == Q6_K; });
     out.push_back(grp);
   }
   return out;
