@@ -28,6 +28,7 @@
 // result (times the next RMSNorm weight) for the next matvec. Nothing synchronizes across
 // workgroups inside a launch: on MI355X each XCD has its own L2, and device-scope fences
 // write back and invalidate it.
+#include <chrono>
 #include <cstdlib>
 #include <map>
 #include <mutex>
@@ -817,6 +818,14 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
   return mv_launch(s, t, n, x, epi, out, nullptr);
 }
 
+// Holds the stream for `ticks` of the constant-rate wall clock, so the launches queued
+// behind it run back to back however slowly the host submits them (a profiler, a busy host).
+// Bounded: the loop also ends after 2^16 sleeps.
+__global__ void k_hold(long long ticks) {
+  const long long t0 = wall_clock64();
+  for (uint32_t i = 0; i < (1u << 16) && wall_clock64() - t0 < ticks; i++) __builtin_amdgcn_s_sleep(63);
+}
+
 // Candidates keep the cost model's K split (NS slices of NSB units, so the staged activation
 // and the order in which every row's products are summed do not change: all candidates give
 // the same bits) and vary the rows per workgroup (NR groups of ITER steps) and the pipeline
@@ -858,18 +867,31 @@ hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t
   hipEvent_t e0 = nullptr, e1 = nullptr;
   WGD_HIP(hipEventCreate(&e0));
   hipError_t err = hipEventCreate(&e1);
+  int dev = 0, khz = 0;
+  if (err == hipSuccess) err = hipGetDevice(&dev);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
   MVPlan best = base;
   double best_us = 1e30;
   const uint32_t reps = nsets < 8 ? 16 : 2 * nsets;
+  double hold_us = 50.0 + 8.0 * reps;  // longer than the host takes to queue the timed launches
   for (const MVPlan &p : cands) {
-    if (err != hipSuccess) break;
-    for (uint32_t i = 0; i < 2 && err == hipSuccess; i++) err = mv_launch(s, sets + n * (i % nsets), n, x, epi, out, &p);
-    if (err == hipSuccess) err = hipEventRecord(e0, s);
-    for (uint32_t i = 0; i < reps && err == hipSuccess; i++) err = mv_launch(s, sets + n * (i % nsets), n, x, epi, out, &p);
-    if (err == hipSuccess) err = hipEventRecord(e1, s);
-    if (err == hipSuccess) err = hipEventSynchronize(e1);
     float ms = 0.f;
-    if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+    for (int attempt = 0; attempt < 4 && err == hipSuccess; attempt++) {
+      for (uint32_t i = 0; i < 2 && err == hipSuccess; i++) err = mv_launch(s, sets + n * (i % nsets), n, x, epi, out, &p);
+      if (err == hipSuccess) {
+        hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, s, (long long)(hold_us * khz / 1000.0));
+        err = hipGetLastError();
+      }
+      const auto t0 = std::chrono::steady_clock::now();
+      if (err == hipSuccess) err = hipEventRecord(e0, s);
+      for (uint32_t i = 0; i < reps && err == hipSuccess; i++) err = mv_launch(s, sets + n * (i % nsets), n, x, epi, out, &p);
+      if (err == hipSuccess) err = hipEventRecord(e1, s);
+      const double queued_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+      if (err == hipSuccess) err = hipEventSynchronize(e1);
+      if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+      if (queued_us < 0.7 * hold_us) break;  // every timed launch was queued before the hold ended
+      hold_us = std::min(2.0 * queued_us + 50.0, 200000.0);
+    }
     // a candidate must beat the cost model's plan by more than timing noise
     const double us = (double)ms * 1e3 / reps * (&p == &cands[0] ? 0.98 : 1.0);
     if (err == hipSuccess && us < best_us) { best_us = us; best = p; }
