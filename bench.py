@@ -257,6 +257,33 @@ def cpu_baseline(f: np.ndarray, title: str, seconds: float = 15.0) -> dict:
                       f"in {dt:.1f} s on {orc.threads()} threads of {cpu}"}
 
 
+def trace_summary(directory: str) -> None:
+    """Per-token kernel table of an `--eager` decode run traced by `rocprofv3 --kernel-trace
+    --output-format csv -d DIR`: every kernel from the first decode token's `k_token_start`
+    on, grouped by name and grid, with launches and microseconds per token."""
+    import collections
+    import csv
+    import glob
+    path = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)[0]
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    first = next(i for i, r in enumerate(rows) if "k_token_start" in r["Kernel_Name"])
+    dec = rows[first:]
+    ntok = sum(1 for r in dec if "k_token_start" in r["Kernel_Name"])
+    agg = collections.defaultdict(list)
+    for r in dec:
+        name = r["Kernel_Name"].split("(")[0][:90] or "(unnamed)"
+        grid = f'{int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"])}x{r["Workgroup_Size_X"]}'
+        agg[(name, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    tot = sum(sum(v) for v in agg.values())
+    span = (int(dec[-1]["End_Timestamp"]) - int(dec[0]["Start_Timestamp"])) / 1e3
+    print(f"decode tokens {ntok}; kernel time {tot / ntok:.1f} us/token; span {span / ntok:.1f} us/token "
+          "(eager, host round trip per token)")
+    print("| kernel | grid (wg x threads) | launches / token | mean us | us / token | share |")
+    print("|---|---|---|---|---|---|")
+    for (k, g), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{k}` | {g} | {len(v) / ntok:.2f} | {sum(v) / len(v):.2f} | {sum(v) / ntok:.1f} | {100 * sum(v) / tot:.1f}% |")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -270,6 +297,8 @@ def main() -> None:
                          "graph replays: for kernel traces, whose profiler does not follow graph launches; the "
                          "tok/s of such a run is not the metric")
     ap.add_argument("--no-attention-timing", action="store_true", help="skip the decode attention timing")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="print the per-token kernel table of an --eager decode traced into DIR by rocprofv3, then exit")
     ap.add_argument("--kv", default="f32", choices=["f32", "f16"],
                     help="K/V ring element type (f32 as the reference; f16 halves the ring bytes)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -284,6 +313,9 @@ def main() -> None:
                     help="only the device sampler (T 0.7, top-k 40, top-p 0.9) on normal logits rows of three vocabulary "
                          "sizes, 30 draws each, no JSON line")
     a = ap.parse_args()
+    if a.trace_summary:
+        trace_summary(a.trace_summary)
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the token loop runs on a single MI355X (multi-GPU sharding is a design "
               "only); run with --gpus 1.", file=sys.stderr)
