@@ -91,7 +91,10 @@ def test_matmul_offsets_all_types(gpu, type_, batch):
         gpu.destroy(buf)
 
 
-@pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 1024, 14336), (Q4_K, 3072, 1024),
+# the three Q4_K microbench shapes (4096x4096, 14336 -> 4096, 4096 -> 14336) and the Q6_K head
+# (4096 -> 128256) as the bench launches them, then shapes off the whole-tile grid
+@pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 4096, 14336), (Q4_K, 14336, 4096),
+                                             (Q6_K, 128256, 4096), (Q4_K, 1024, 14336), (Q4_K, 3072, 1024),
                                              (Q6_K, 1024, 4096), (Q6_K, 520, 5376), (Q8_0, 512, 4096),
                                              (Q4_K, 300, 3072), (Q5_K, 1024, 4096), (Q5_K, 520, 14336),
                                              (Q4_0, 512, 4096), (Q4_0, 300, 3136), (F16, 4096, 4096),
