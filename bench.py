@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 
 from webgpu_amd import synth  # noqa: E402
 from webgpu_amd.engine import LoadOptions, PagedEngine  # noqa: E402
-from webgpu_amd.gguf import F16, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS  # noqa: E402
+from webgpu_amd.gguf import F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS  # noqa: E402
 from webgpu_amd.gpu import Compute  # noqa: E402
 
 PEAK_HBM = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
@@ -118,7 +118,8 @@ def matvec_bench(gpu: Compute, ev: Events, type_: int, cols: int, rows: int, lau
     if type_ in (Q4_K, Q6_K):
         base = (synth.microbench_q4k if type_ == Q4_K else synth.microbench_q6k)(rng, rows, cols)
     else:
-        gen = {Q5_K: synth.q5k_blocks, Q8_0: synth.q8_0_blocks, Q4_0: synth.q4_0_blocks, F16: synth.f16_values}[type_]
+        gen = {Q5_K: synth.q5k_blocks, Q8_0: synth.q8_0_blocks, Q4_0: synth.q4_0_blocks, F16: synth.f16_values,
+               F32: lambda r, n: (r.standard_normal(n) * 0.02).astype(np.float32).view(np.uint8)}[type_]
         base = gen(rng, rows * cols // q["block"])
     ws = []
     for i in range(copies):
@@ -334,7 +335,7 @@ def main() -> None:
         # the roofline shapes, then the FFN-up shape in every type with a planar layout
         for s in [(Q4_K, 14336, 4096), (Q4_K, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 4096, 128256),
                   (Q5_K, 14336, 4096), (Q6_K, 14336, 4096), (Q8_0, 14336, 4096), (Q4_0, 14336, 4096),
-                  (F16, 14336, 4096)]:
+                  (F16, 14336, 4096), (F32, 14336, 4096)]:
             m = matvec_bench(gpu, ev, *s)
             print(f"[bench] matvec {m['type']} {m['shape']}: {m['us']:.2f} us, {m['GBps']:.0f} GB/s "
                   f"({100 * m['frac']:.1f}% of 8 TB/s)", file=sys.stderr, flush=True)

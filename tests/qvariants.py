@@ -12,8 +12,11 @@ the three shaped decoders do not use.
   Q6_K V (one Q/K/V launch of two types), Q4_0 O, down and embedding table.
 * ``qwen3-f16``: every matrix F16 (the GGUF row-major layout: the F16 decode matvec and
   the generic prompt GEMM), with Q/K norm.
+* ``llama-q80-w96``: every matrix Q8_0 at hidden width 96, which is not a whole 64-column
+  tile: the matrices reading the hidden state keep the GGUF layout, so decode runs the
+  generic step (batched kernels at one token, the position read from device state).
 
-Dimensions are the smallest the planar K-quant kernels take: hidden 256 (Q4_K/Q6_K rows of
+Dimensions (but for ``llama-q80-w96``) are the smallest the planar K-quant kernels take: hidden 256 (Q4_K/Q6_K rows of
 whole 256-element blocks), 4 query heads x 64, 2 KV heads, FFN 512, vocab 300. Matrix blocks
 come from the synthetic generators (webgpu_amd/synth.py); norm and bias vectors are f32.
 """
@@ -25,7 +28,7 @@ from webgpu_amd import synth
 from webgpu_amd.gguf import F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
 from webgpu_amd.tokenizer import byte_alphabet
 
-KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16")
+KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16", "llama-q80-w96")
 
 
 CHAT_SPECIALS = ["<|im_start|>", "<|im_end|>", "<|endoftext|>"]
@@ -50,8 +53,11 @@ def build(kind: str, tokenizer: bool = False):
     file also carries a byte-level BPE vocabulary with a ChatML template."""
     rng = np.random.default_rng(sum(kind.encode()) * 31 + 5)
     H, nh, nkv, hd, F, V, L = 256, 4, 2, 64, 512, 300, 2
+    w96 = kind == "llama-q80-w96"
+    if w96:
+        H = 96
     arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3", "llama-q5q4": "llama",
-            "qwen3-f16": "qwen3"}[kind]
+            "qwen3-f16": "qwen3", "llama-q80-w96": "llama"}[kind]
     qd, kd = nh * hd, nkv * hd
     T: List[Tuple[str, List[int], int, np.ndarray]] = []
 
@@ -66,12 +72,12 @@ def build(kind: str, tokenizer: bool = False):
         T.append((name, [n], F32, v.view(np.uint8)))
 
     q5, f16 = kind == "llama-q5q4", kind == "qwen3-f16"
-    mat("token_embd.weight", H, V, Q4_0 if q5 else F16 if f16 else Q6_K, 0.5)
+    mat("token_embd.weight", H, V, Q4_0 if q5 else F16 if f16 else Q8_0 if w96 else Q6_K, 0.5)
     vec("output_norm.weight", H)
-    mat("output.weight", H, V, Q5_K if q5 else F16 if f16 else Q6_K, 0.3)
-    k_type = Q8_0 if kind == "qwen3-mixed" else Q5_K if q5 else F16 if f16 else Q4_K
-    big, small = (Q5_K, Q4_0) if q5 else (F16, F16) if f16 else (Q4_K, Q4_K)
-    v_type = F16 if f16 else Q6_K
+    mat("output.weight", H, V, Q5_K if q5 else F16 if f16 else Q8_0 if w96 else Q6_K, 0.3)
+    k_type = Q8_0 if kind in ("qwen3-mixed", "llama-q80-w96") else Q5_K if q5 else F16 if f16 else Q4_K
+    big, small = (Q5_K, Q4_0) if q5 else (F16, F16) if f16 else (Q8_0, Q8_0) if w96 else (Q4_K, Q4_K)
+    v_type = F16 if f16 else Q8_0 if w96 else Q6_K
     for l in range(L):
         p = f"blk.{l}."
         vec(p + "attn_norm.weight", H)
@@ -104,7 +110,7 @@ def build(kind: str, tokenizer: bool = False):
     elif kind == "llama-partial":
         meta += [(f"{arch}.rope.freq_base", 6, 1e4), (f"{arch}.rope.dimension_count", 4, 32),
                  (f"{arch}.attention.sliding_window", 4, 24)]
-    elif kind == "llama-q5q4":
+    elif kind in ("llama-q5q4", "llama-q80-w96"):
         meta += [(f"{arch}.rope.freq_base", 6, 5e5), (f"{arch}.rope.dimension_count", 4, hd)]
     else:
         meta += [(f"{arch}.rope.freq_base", 6, 1e6), (f"{arch}.rope.dimension_count", 4, 48),

@@ -21,7 +21,8 @@ pytestmark = pytest.mark.gpu
 ALL = [F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K]
 # synthetic block generators of the types with a decode matvec
 GEN = {Q4_K: synth.q4k_blocks, Q5_K: synth.q5k_blocks, Q6_K: synth.q6k_blocks, Q8_0: synth.q8_0_blocks,
-       Q4_0: synth.q4_0_blocks, F16: synth.f16_values}
+       Q4_0: synth.q4_0_blocks, F16: synth.f16_values,
+       F32: lambda rng, n, std=0.05: (rng.standard_normal(n) * std).astype(np.float32).view(np.uint8)}
 
 
 def near(got, want, tol=1e-3, label=""):
@@ -98,7 +99,8 @@ def test_matmul_offsets_all_types(gpu, type_, batch):
                                              (Q6_K, 1024, 4096), (Q6_K, 520, 5376), (Q8_0, 512, 4096),
                                              (Q4_K, 300, 3072), (Q5_K, 1024, 4096), (Q5_K, 520, 14336),
                                              (Q4_0, 512, 4096), (Q4_0, 300, 3136), (F16, 4096, 4096),
-                                             (F16, 1030, 14336), (F16, 300, 3072)])
+                                             (F16, 1030, 14336), (F16, 300, 3072), (F32, 4096, 4096),
+                                             (F32, 1030, 14336), (F32, 300, 3072), (F32, 256, 64)])
 def test_fast_matvec_real_shapes(gpu, type_, rows, cols):
     rng = np.random.default_rng(rows + cols)
     gen = GEN[type_]
@@ -378,7 +380,8 @@ def test_bounds_checks_reject_overruns(gpu):
 
 # ---------------------------------------------------------------- quantized activation + matvec entries
 @pytest.mark.parametrize("type_,rows,cols", [(Q4_K, 512, 4096), (Q6_K, 256, 5376), (Q8_0, 128, 1024),
-                                             (Q5_K, 256, 4096), (Q4_0, 128, 2048), (F16, 200, 2048)])
+                                             (Q5_K, 256, 4096), (Q4_0, 128, 2048), (F16, 200, 2048),
+                                             (F32, 200, 2048)])
 def test_quantize_with_rms_norm_then_matvec(gpu, type_, rows, cols):
     """wgd_quantize(x, norm w) + wgd_matvec == W @ (x * rsqrt(mean(x^2) + eps) * w)."""
     rng = np.random.default_rng(rows)

@@ -541,16 +541,17 @@ __global__ __launch_bounds__(1024) void k_mv(MV m) {
   else mv_tile<T1, DU, GLU>(m, g, t, lds);
 }
 
-// ------------------------------------------------------------------ F16 weights
+// ------------------------------------------------------------------ F16 and F32 weights
 //
-// F16 matrices keep the GGUF row-major layout (a row is K contiguous halves, 16-byte
-// aligned for K % 8 == 0) and take the same QX activation, epilogues and launch groups as the
-// integer kernel. A workgroup of four wavefronts owns RT rows (RT / 4 per wavefront, four at a
-// time): the activation is rebuilt in LDS as f32 from its digits (the exact integer
-// d0 * 254^2 + d1 * 254 + d2 times scale / 254^2, as the integer kernel combines them), each
-// lane reads 8 halves of each of four rows per step (a wavefront reads 1 KB of a row), and
-// multiplies them in f32 with the activation (the reference's arithmetic, shaders.ts:39-54);
-// the row sums are reduced across the wavefront and finished by the epilogue threads.
+// F16 and F32 matrices keep the GGUF row-major layout (a row is K contiguous halves or
+// floats, 16-byte aligned for K % 8 == 0) and take the same QX activation, epilogues and
+// launch groups as the integer kernel. A workgroup of four wavefronts owns RT rows (RT / 4
+// per wavefront, four at a time): the activation is rebuilt in LDS as f32 from its digits
+// (the exact integer d0 * 254^2 + d1 * 254 + d2 times scale / 254^2, as the integer kernel
+// combines them), each lane reads 8 elements of each of four rows per step (one 16-byte load
+// of halves, two of floats: a wavefront reads 1 or 2 KB of a row), and multiplies them in
+// f32 with the activation (the reference's arithmetic, shaders.ts:39-54); the row sums are
+// reduced across the wavefront and finished by the epilogue threads.
 constexpr uint32_t MV16_THREADS = 256;
 
 __device__ __forceinline__ float dot8_f16(const uint4 &w, const float4 &a, const float4 &b) {
@@ -564,7 +565,19 @@ __device__ __forceinline__ float dot8_f16(const uint4 &w, const float4 &a, const
   return fmaf(f16hi(w.w), b.w, s);
 }
 
-template <bool GLU>
+__device__ __forceinline__ float dot8_f32(const uint4 &w0, const uint4 &w1, const float4 &a, const float4 &b) {
+  float s = __uint_as_float(w0.x) * a.x;
+  s = fmaf(__uint_as_float(w0.y), a.y, s);
+  s = fmaf(__uint_as_float(w0.z), a.z, s);
+  s = fmaf(__uint_as_float(w0.w), a.w, s);
+  s = fmaf(__uint_as_float(w1.x), b.x, s);
+  s = fmaf(__uint_as_float(w1.y), b.y, s);
+  s = fmaf(__uint_as_float(w1.z), b.z, s);
+  return fmaf(__uint_as_float(w1.w), b.w, s);
+}
+
+// ES: bytes per weight element (2: F16, 4: F32).
+template <bool GLU, int ES>
 __global__ __launch_bounds__(MV16_THREADS) void k_mv16(MV m) {
   extern __shared__ __attribute__((aligned(16))) float l16[];
   uint32_t t = blockIdx.x;
@@ -605,19 +618,28 @@ __global__ __launch_bounds__(MV16_THREADS) void k_mv16(MV m) {
     float a[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
     for (uint32_t k = lane * 8; k < K; k += 512) {
-      uint4 wq[4], wq1[4];
+      constexpr int NL = ES / 2;  // 16-byte loads per row and step
+      uint4 wq[4][NL], wq1[4][NL];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         // rows past the matrix read zero (offsets past the buffer range)
-        const uint32_t off = ((row0 + r0 + j) * K + k) * 2;
-        wq[j] = bl16(rw, off, 0);
-        if (GLU) wq1[j] = bl16(rw1, off, 0);
+        const uint32_t off = ((row0 + r0 + j) * K + k) * ES;
+#pragma unroll
+        for (int h = 0; h < NL; h++) {
+          wq[j][h] = bl16(rw, off + 16 * h, 0);
+          if (GLU) wq1[j][h] = bl16(rw1, off + 16 * h, 0);
+        }
       }
       const float4 x0 = *(const float4 *)(xs + k), x1 = *(const float4 *)(xs + k + 4);
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        a[j] += dot8_f16(wq[j], x0, x1);
-        if (GLU) a1[j] += dot8_f16(wq1[j], x0, x1);
+        if constexpr (ES == 2) {
+          a[j] += dot8_f16(wq[j][0], x0, x1);
+          if (GLU) a1[j] += dot8_f16(wq1[j][0], x0, x1);
+        } else {
+          a[j] += dot8_f32(wq[j][0], wq[j][NL - 1], x0, x1);
+          if (GLU) a1[j] += dot8_f32(wq1[j][0], wq1[j][NL - 1], x0, x1);
+        }
       }
     }
 #pragma unroll
@@ -675,10 +697,14 @@ hipError_t quantize(hipStream_t s, const float *x, uint32_t K, const float *norm
   return hipGetLastError();
 }
 
-// F16 rows of up to 32768 halves (the f32 activation fits in LDS), 32-bit buffer offsets.
+static bool float_type(int t) { return t == F16 || t == F32; }
+static uint32_t float_bytes(int t) { return t == F32 ? 4 : 2; }
+
+// F16 / F32 rows of up to 32768 elements (the f32 activation fits in LDS), 32-bit buffer
+// offsets.
 static bool mv16_supported(const Matrix &w) {
-  return w.type == F16 && w.layout == LAYOUT_GGUF && w.cols && w.rows && w.cols % 16 == 0 && w.cols <= 32768 &&
-         ((uint64_t)w.rows + 64) * w.cols * 2 < (1ull << 31);
+  return float_type(w.type) && w.layout == LAYOUT_GGUF && w.cols && w.rows && w.cols % 16 == 0 && w.cols <= 32768 &&
+         ((uint64_t)w.rows + 64) * w.cols * float_bytes(w.type) < (1ull << 31);
 }
 
 // Row tiles of 64, 32 or 16 rows: the largest that still gives every CU a workgroup.
@@ -699,7 +725,7 @@ static MVPlan mv16_plan(const Matrix &w, const uint32_t *rows, uint32_t n) {
 }
 
 bool mv_supported(const Matrix &w) {
-  if (w.type == F16) return mv16_supported(w);
+  if (float_type(w.type)) return mv16_supported(w);
   if (w.layout != LAYOUT_PLANAR || !w.cols || !w.rows) return false;
   if (w.type == Q4_K || w.type == Q5_K || w.type == Q6_K) return w.cols % 256 == 0;
   if (w.type == Q8_0 || w.type == Q4_0) return w.cols % 32 == 0;
@@ -726,7 +752,7 @@ uint32_t mv_arg_entries(const Matrix &w) {
 // only queues), when the activation staging is amortised over few rows, and for idle chunk
 // columns.
 MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out) {
-  if (w.type == F16) return mv16_plan(w, rows, n);
+  if (float_type(w.type)) return mv16_plan(w, rows, n);
   MVPlan best_p{};
   const uint32_t N = chunk_elems(w.type), C = w.cols / N, CQ = (C + 7) / 8;
   const uint32_t cus = (uint32_t)device_cu_count();
@@ -835,7 +861,7 @@ hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t
                    const MVOut *out) {
   if (!nsets || n < 1 || n > (uint32_t)MV_MAX_SEGS) return hipErrorInvalidValue;
   const Matrix &w0 = *sets[0].w;
-  if (w0.type == F16 || (out && out->arg_part)) return hipSuccess;  // F16 and the head keep the model's plan
+  if (float_type(w0.type) || (out && out->arg_part)) return hipSuccess;  // F16/F32 and the head keep the model's plan
   const bool glu = sets[0].w1 != nullptr, qout = out && out->q.d0;
   const PlanKey key = plan_key(sets, n, epi, qout);
   {
@@ -914,11 +940,12 @@ static hipError_t mv_launch(hipStream_t s, const MVTarget *t, uint32_t n, const 
   if ((epi == MV_SILU || epi == MV_GELU) != glu) return hipErrorInvalidValue;
   if (x.len != w0.cols) return hipErrorInvalidValue;
   uint32_t rows[MV_MAX_SEGS];
-  if (w0.type == F16) {
+  if (float_type(w0.type)) {
     for (uint32_t i = 0; i < n; i++) {
       const Matrix &w = *t[i].w;
-      if (!mv16_supported(w) || w.cols != w0.cols || !t[i].y || (t[i].w1 != nullptr) != glu) return hipErrorInvalidValue;
-      if (glu && (t[i].w1->type != F16 || t[i].w1->layout != w.layout || t[i].w1->cols != w.cols ||
+      if (!mv16_supported(w) || w.type != w0.type || w.cols != w0.cols || !t[i].y || (t[i].w1 != nullptr) != glu)
+        return hipErrorInvalidValue;
+      if (glu && (t[i].w1->type != w.type || t[i].w1->layout != w.layout || t[i].w1->cols != w.cols ||
                   t[i].w1->rows != w.rows))
         return hipErrorInvalidValue;
       rows[i] = w.rows;
@@ -930,7 +957,7 @@ static hipError_t mv_launch(hipStream_t s, const MVTarget *t, uint32_t n, const 
     for (uint32_t i = 0; i < n; i++) {
       MVSeg &g = m.seg[i];
       g.w = t[i].w->data; g.w1 = glu ? t[i].w1->data : nullptr;
-      g.bytes = (uint32_t)((uint64_t)rows[i] * w0.cols * 2);
+      g.bytes = (uint32_t)((uint64_t)rows[i] * w0.cols * float_bytes(w0.type));
       g.y = t[i].y; g.bias = t[i].bias; g.rows = rows[i];
       g.tiles = (rows[i] + p.RT - 1) / p.RT;
     }
@@ -946,7 +973,8 @@ static hipError_t mv_launch(hipStream_t s, const MVTarget *t, uint32_t n, const 
       hipLaunchKernelGGL(kernel, dim3(p.tiles), dim3(MV16_THREADS), p.lds, s, m);
       return hipGetLastError();
     };
-    return glu ? go(k_mv16<true>) : go(k_mv16<false>);
+    if (w0.type == F32) return glu ? go(k_mv16<true, 4>) : go(k_mv16<false, 4>);
+    return glu ? go(k_mv16<true, 2>) : go(k_mv16<false, 2>);
   }
   // Q6_K segments may share a launch with Q4_K or Q5_K ones (same chunk shape); other
   // types run alone

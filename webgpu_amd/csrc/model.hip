@@ -556,8 +556,9 @@ hipError_t decode_step_q(wgd_model *m, bool advance) {
   return hipGetLastError();
 }
 
-// One decode step with n = 1 for models whose matrices the quantized matvec does not read
-// (F32, F16, Q4_0, Q5_K): the batched kernels with the position read from device state.
+// One decode step with n = 1 for models with a matrix the decode matvec does not read (Q8_0
+// or Q4_0 widths off the 64-column planar tile, float rows of a width off 16 elements): the
+// batched kernels with the position read from device state.
 hipError_t decode_step_generic(wgd_model *m, bool advance) {
   hipStream_t s = m->ctx->stream;
   WGD_HIP(embed_matrix(s, m->embd, &m->state->token, m->hidden, 1, m->c.embed_scale));
