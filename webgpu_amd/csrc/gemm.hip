@@ -231,18 +231,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 // workgroup owns QG_M = 128 weight rows x QG_N = 128 tokens and a K span (split-K when the
 // rows alone give too few workgroups; partial sums are added in split order by
 // k_gemm_reduce, so results do not depend on timing). The activations are split into bf16
-// (hi, lo) once per input by k_gemm_split, already in MFMA fragment order, so a
-// workgroup's activation tile is a plain 32 KB copy. Per 64-column K tile every weight of
-// the workgroup's rows is dequantized once, from coalesced 16-byte planar loads (one
-// 32-element chunk of one row per thread), split the same way and stored in fragment
-// order. Four wavefronts each compute 64 rows x 64 tokens, sixteen 16 x 16 accumulators,
-// three MFMAs per product (hi*hi + hi*lo + lo*hi). The next K tile's loads are issued
-// before the MFMAs of the current one; 64 KB of LDS lets two workgroups share a CU, so
-// one's dequantization overlaps the other's MFMAs.
+// (hi, lo) once per input by k_gemm_split, already in MFMA fragment order, so each
+// wavefront loads its activation fragments of a K tile straight from that buffer (L2
+// hits: every workgroup of the launch reads the same tiles) into registers, 1 KB per load
+// instruction, before the tile's dequantization. Per 64-column K tile every weight of the
+// workgroup's rows is dequantized once, from coalesced 16-byte planar loads (one 32-element
+// chunk of one row per thread), split the same way and stored in LDS in fragment order.
+// Four wavefronts each compute 64 rows x 64 tokens, sixteen 16 x 16 accumulators, three
+// MFMAs per product (hi*hi + hi*lo + lo*hi). The next K tile's weight loads are issued
+// before the MFMAs of the current one; two workgroups share a CU (the register budget of
+// the launch bounds), so one's dequantization can run beside the other's MFMAs.
 //
 // The weight tile is kept in LDS in the activations' fragment order (split.h), as rows.
 constexpr uint32_t QG_M = 128, QG_N = SPLIT_N, QG_K = SPLIT_K, QG_TILE = SPLIT_TILE;
-constexpr uint32_t QG_LDS = 2 * QG_TILE * 2;  // bytes: weight tile + activation tile
+constexpr uint32_t QG_LDS = QG_TILE * 2;  // bytes: weight tile
 
 // One weight matrix of a grouped launch: its planar geometry, the row-tile count, and where
 // its rows go (y, or rows [row0, row0 + rows) of the group's split-K partial sums).
@@ -413,23 +415,23 @@ template <> struct QWeights<Q4_0> {
 
 template <int TYPE>
 __device__ __forceinline__ void gemm_tile(const QGemm &a, const QJob &jb, uint32_t mt, uint16_t *qlds) {
-  uint16_t *wt = qlds, *xt = qlds + QG_TILE;
+  uint16_t *wt = qlds;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv & 1, wn = wv >> 1;
   const uint32_t m0 = mt * QG_M, n0 = blockIdx.y * QG_N, z = blockIdx.z;
   const uint32_t kb = z * a.kspan, ke = kb + a.kspan < a.cols ? kb + a.kspan : a.cols;
   const QRsrc rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(jb.w), 0, (int)jb.wbytes, 0x00020000);
   // this thread's weights: row tile wrt, 32-column half wcc of the K tile, row wr
   const uint32_t wrt = tid >> 5, wcc = (tid >> 4) & 1, wr = tid & 15;
-  // this thread's activation copy: 16-byte chunks tid + 256 i of the tile
-  const uint16_t *xsrc = a.xs + (uint64_t)blockIdx.y * (a.cols / QG_K) * QG_TILE + 8 * tid;
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const uint32_t ktiles = a.cols / QG_K;
+  const QRsrc rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.xs + (uint64_t)blockIdx.y * ktiles * QG_TILE), 0, (int)(ktiles * QG_TILE * 2), 0x00020000);
   QWeights<TYPE> wreg;
-  u32x4 xr[8];
-  auto fetch = [&](uint32_t k0) {
-    wreg.fetch(jb, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc);
-    const uint16_t *src = xsrc + (uint64_t)(k0 / QG_K) * QG_TILE;
-#pragma unroll
-    for (int i = 0; i < 8; i++) xr[i] = *(const u32x4 *)(src + 2048 * i);
+  auto fetch = [&](uint32_t k0) { wreg.fetch(jb, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc); };
+  // this wavefront's activation fragments of a K tile, from the split buffer
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  auto xfrag = [&](uint32_t k0, uint32_t hl, uint32_t b, uint32_t ks) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+        rx, 2 * ((k0 / QG_K) * QG_TILE + frag_at(hl, b, ks, 0, 0) + 8 * lane), 0, 0));
   };
   auto stage = [&](uint32_t k0) {
     float v[32];
@@ -442,8 +444,6 @@ __device__ __forceinline__ void gemm_tile(const QGemm &a, const QJob &jb, uint32
       *(uint4 *)(wt + frag_at(0, wrt, wcc, g, wr)) = make_uint4(h[4 * g], h[4 * g + 1], h[4 * g + 2], h[4 * g + 3]);
       *(uint4 *)(wt + frag_at(1, wrt, wcc, g, wr)) = make_uint4(l[4 * g], l[4 * g + 1], l[4 * g + 2], l[4 * g + 3]);
     }
-#pragma unroll
-    for (int i = 0; i < 8; i++) *(u32x4 *)(xt + 8 * tid + 2048 * i) = xr[i];
   };
   f32x4 acc[4][4];
 #pragma unroll
@@ -452,26 +452,32 @@ __device__ __forceinline__ void gemm_tile(const QGemm &a, const QJob &jb, uint32
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   fetch(kb);
   for (uint32_t k0 = kb; k0 < ke; k0 += QG_K) {
+    bf16x8 Bh[2][4], Bl[2][4];
+#pragma unroll
+    for (uint32_t ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) {
+        Bh[ks][i] = xfrag(k0, 0, wn * 4 + i, ks);
+        Bl[ks][i] = xfrag(k0, 1, wn * 4 + i, ks);
+      }
     stage(k0);
     __syncthreads();
     if (k0 + QG_K < ke) fetch(k0 + QG_K);  // next tile's loads fly during the MFMAs
 #pragma unroll
     for (uint32_t ks = 0; ks < 2; ks++) {
-      bf16x8 Ah[4], Al[4], Bh[4], Bl[4];
+      bf16x8 Ah[4], Al[4];
 #pragma unroll
       for (uint32_t i = 0; i < 4; i++) {
         Ah[i] = *(const bf16x8 *)(wt + frag_at(0, wm * 4 + i, ks, 0, 0) + 8 * lane);
         Al[i] = *(const bf16x8 *)(wt + frag_at(1, wm * 4 + i, ks, 0, 0) + 8 * lane);
-        Bh[i] = *(const bf16x8 *)(xt + frag_at(0, wn * 4 + i, ks, 0, 0) + 8 * lane);
-        Bl[i] = *(const bf16x8 *)(xt + frag_at(1, wn * 4 + i, ks, 0, 0) + 8 * lane);
       }
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[j], Ah[i], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bl[j], Ah[i], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[j], Al[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[ks][j], Ah[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bl[ks][j], Ah[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[ks][j], Al[i], acc[i][j], 0, 0, 0);
         }
     }
     __syncthreads();
@@ -592,7 +598,7 @@ bool gemm_group_ok(const GemmGroup &g, uint32_t batch) {
   return group_types(g, t) && qgemm_pair(t[0], t[1]);
 }
 
-// K span per workgroup: enough splits for two workgroups per CU (64 KB of LDS each), each
+// K span per workgroup: enough splits for two workgroups per CU, each
 // at least one 256-column block (64 columns when every matrix is Q8_0), and no more partial
 // sums than the scratch holds.
 static uint32_t group_kspan(const GemmGroup &g, uint32_t batch, uint64_t scratch_floats, uint32_t *rows_total) {
