@@ -428,7 +428,6 @@ __device__ __forceinline__ void gemm_tile(const QGemm &a, const QJob &jb, uint32
   QWeights<TYPE> wreg;
   auto fetch = [&](uint32_t k0) { wreg.fetch(jb, rw, m0 / 16 + wrt, wr, k0 / 32 + wcc); };
   // this wavefront's activation fragments of a K tile, from the split buffer
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   auto xfrag = [&](uint32_t k0, uint32_t hl, uint32_t b, uint32_t ks) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
         rx, 2 * ((k0 / QG_K) * QG_TILE + frag_at(hl, b, ks, 0, 0) + 8 * lane), 0, 0));
