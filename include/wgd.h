@@ -70,10 +70,10 @@ int wgd_buffer_create(wgd_context *ctx, uint64_t size, const char *label, wgd_bu
 int wgd_buffer_destroy(wgd_context *ctx, wgd_buffer *buf);
 uint64_t wgd_buffer_size(const wgd_buffer *buf);
 /* WeightPager.page (pager.ts:25-44) with paging collapsed: upload a whole rows x cols weight
- * matrix of GGUF `type` once, in the layout the kernels read fastest. Q4_K, Q6_K and Q8_0
- * are rearranged on the device into a planar layout of the same bits (16-byte quant chunks
- * tiled by 16 rows, block headers/scales in separate planes); other types keep the GGUF
- * bytes. Decoded values are unchanged. The buffer is accepted by wgd_matmul, wgd_matvec and
+ * matrix of GGUF `type` once, in the layout the kernels read fastest. Q4_K, Q5_K and Q6_K
+ * (and Q8_0 / Q4_0 of a width that is a multiple of 64) are rearranged on the device into a
+ * planar layout of the same bits (16-byte quant chunks tiled by 16 rows, block headers and
+ * scales in separate planes); other types keep the GGUF bytes. Decoded values are unchanged. The buffer is accepted by wgd_matmul, wgd_matvec and
  * wgd_embed for that type and shape. `bytes` must equal rows*rowBytes. */
 int wgd_upload_weights(wgd_context *ctx, int32_t type, uint32_t cols, uint32_t rows,
                        const void *data, uint64_t bytes, const char *label, wgd_buffer **out);
@@ -98,8 +98,10 @@ int wgd_done(wgd_context *ctx);
 /* matmulShader(type) (shaders.ts:39-54), dispatched by `linear` (engine.ts:125-137):
  *   y[b*stride + rowBase + r] = sum_c deq(W)[r*cols + c] * x[(b+inputOffset)*cols + c]
  * for r < rows, b < batch. W holds GGUF blocks of `type` (rows x cols, row-major,
- * quantized along cols). Batch 1-4 runs the dequant-matvec; larger batches run the
- * dequant-GEMM on bf16 MFMA with a split-precision activation operand. */
+ * quantized along cols). Batch 1 runs the decode matvec (wgd_quantize + wgd_matvec) where
+ * the type and layout allow it; batches above 4, and any batch on planar weights, run the
+ * dequant-GEMM on bf16 MFMA with a split-precision activation operand; the rest runs a
+ * generic f32 kernel. */
 int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *x,
                wgd_buffer *y, uint32_t cols, uint32_t rows, uint32_t stride, uint32_t row_base,
                uint32_t input_offset, uint32_t batch);
@@ -108,7 +110,8 @@ int wgd_matmul(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
  * integer matvec reads (buffer of wgd_quantized_bytes(cols)), optionally as RMSNorm(x) * w
  * (normShader, shaders.ts:55-68, with w = norm_weight, NULL for none); wgd_matvec then
  * computes y[row_base + r] = sum_c deq(W)[r][c] x[c] for weights uploaded with
- * wgd_upload_weights (Q4_K, Q6_K, Q8_0). wgd_matmul with batch 1 runs exactly these two. */
+ * wgd_upload_weights (every type; Q8_0 and Q4_0 in the planar layout, F16 and F32 rows of a
+ * width that is a multiple of 16). wgd_matmul with batch 1 runs exactly these two. */
 uint64_t wgd_quantized_bytes(uint32_t cols);
 int wgd_quantize(wgd_context *ctx, const wgd_buffer *x, uint32_t cols, const wgd_buffer *norm_weight,
                  float epsilon, wgd_buffer *qx);
