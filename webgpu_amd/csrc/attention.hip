@@ -177,6 +177,70 @@ __global__ __launch_bounds__(128) void k_attention_combine(const float *part, fl
                  make_float4(out[8 * g + 4], out[8 * g + 5], out[8 * g + 6], out[8 * g + 7]));
 }
 
+// k_attention_combine for at most S splits, the same arithmetic in the same order, with each
+// pass's loads over the splits issued together (raw buffer loads over the partials, zero
+// past the last split, which selects leave out).
+template <uint32_t S>
+__global__ __launch_bounds__(128) void k_attention_combine_s(const float *part, float *y, uint32_t rows, uint32_t hd,
+                                                             uint32_t nsplit, uint16_t *xs, uint32_t heads) {
+  __shared__ float out[512];
+  const uint64_t row = blockIdx.x;
+  const uint64_t stride = (uint64_t)rows * (hd + 2);
+  const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, nsplit, stride);
+  const uint32_t sb = (uint32_t)(4 * stride), rb = (uint32_t)(4 * row * (hd + 2));
+  float mz[S], lz[S];
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) {
+    mz[z] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, rb + z * sb, 0, 0));
+    lz[z] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, rb + z * sb + 4, 0, 0));
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) M = z < nsplit ? fmaxf(M, mz[z]) : M;
+  bool use[S];
+  float wz[S];
+  float L = 0.f;
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) {
+    use[z] = z < nsplit && mz[z] != -INFINITY;
+    wz[z] = use[z] ? expf(mz[z] - M) : 0.f;
+    L = use[z] ? L + lz[z] * wz[z] : L;
+  }
+  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    float pz[S];
+#pragma unroll
+    for (uint32_t z = 0; z < S; z++)
+      pz[z] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, rb + z * sb + 4 * (2 + d), 0, 0));
+    float acc = 0.f;
+#pragma unroll
+    for (uint32_t z = 0; z < S; z++) acc = use[z] ? acc + pz[z] * wz[z] : acc;
+    const float o = L > 0.f ? acc / L : 0.f;
+    y[row * hd + d] = o;
+    out[d] = o;
+  }
+  if (!xs) return;
+  __syncthreads();
+  const uint32_t tok = (uint32_t)(row / heads), h = (uint32_t)(row % heads);
+  for (uint32_t g = threadIdx.x; g < hd / 8; g += blockDim.x)
+    split_store8(xs, heads * hd, tok, h * hd + 8 * g, make_float4(out[8 * g], out[8 * g + 1], out[8 * g + 2], out[8 * g + 3]),
+                 make_float4(out[8 * g + 4], out[8 * g + 5], out[8 * g + 6], out[8 * g + 7]));
+}
+
+// The merge of nsplit key splits: the load-batched kernel when the splits fit it, else the
+// general one.
+static void launch_attention_combine(hipStream_t s, const float *part, float *y, uint32_t rows, uint32_t hd,
+                                     uint32_t nsplit, uint16_t *xs, uint32_t heads) {
+  const bool fits = (uint64_t)nsplit * rows * (hd + 2) * 4 < (1ull << 31);
+  if (fits && nsplit <= 4)
+    hipLaunchKernelGGL(k_attention_combine_s<4>, dim3(rows), dim3(128), 0, s, part, y, rows, hd, nsplit, xs, heads);
+  else if (fits && nsplit <= 8)
+    hipLaunchKernelGGL(k_attention_combine_s<8>, dim3(rows), dim3(128), 0, s, part, y, rows, hd, nsplit, xs, heads);
+  else if (fits && nsplit <= 16)
+    hipLaunchKernelGGL(k_attention_combine_s<16>, dim3(rows), dim3(128), 0, s, part, y, rows, hd, nsplit, xs, heads);
+  else
+    hipLaunchKernelGGL(k_attention_combine, dim3(rows), dim3(128), 0, s, part, y, rows, hd, nsplit, xs, heads);
+}
+
 // Prompt batches on the f32 matrix cores (v_mfma_f32_16x16x4_f32: f32 products, f32 sums, as
 // the f32 shader computes them). A wavefront owns 16 consecutive queries of one head; the
 // four wavefronts of a workgroup share one kv head and stage 64-key tiles of K (row-major)
@@ -334,8 +398,7 @@ static hipError_t launch_attn_prompt(hipStream_t s, AttnK a, const AttnArgs &in,
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
     uint16_t *xs = in.xs && in.hd % 8 == 0 && in.heads * in.hd % 64 == 0 ? in.xs : nullptr;
-    hipLaunchKernelGGL(k_attention_combine, dim3(in.batch * in.heads), dim3(128), 0, s, (const float *)in.partial,
-                       in.y, in.batch * in.heads, in.hd, nsplit, xs, in.heads);
+    launch_attention_combine(s, (const float *)in.partial, in.y, in.batch * in.heads, in.hd, nsplit, xs, in.heads);
     WGD_HIP(hipGetLastError());
     if (in.xs_written) *in.xs_written = xs != nullptr;
   }
@@ -433,8 +496,7 @@ hipError_t attention(hipStream_t s, const AttnArgs &in) {
   }
   WGD_HIP(hipGetLastError());
   if (nsplit > 1) {
-    hipLaunchKernelGGL(k_attention_combine, dim3(in.batch * in.heads), dim3(128), 0, s, (const float *)in.partial,
-                       in.y, in.batch * in.heads, in.hd, nsplit, (uint16_t *)nullptr, in.heads);
+    launch_attention_combine(s, (const float *)in.partial, in.y, in.batch * in.heads, in.hd, nsplit, nullptr, in.heads);
     WGD_HIP(hipGetLastError());
   }
   return hipSuccess;

@@ -115,6 +115,46 @@ __device__ __forceinline__ float segment_sum(float v, int width) {
   return v;
 }
 
+// ------------------------------------------------------------------ split-K partial sums
+// The split-K GEMMs leave partial sums part[z][...] for z < splits (at most MAX_SPLITS),
+// `stride` floats apart. These add one element's (or four consecutive elements') partials
+// in split order, the adds of a loop over z, with every split's load issued before the
+// first add: raw buffer loads over the partial buffer (4 * splits * stride bytes, below
+// 2^31), so the loads of the splits past `splits` read zero without touching memory, and
+// selects leave them out of the sum.
+constexpr uint32_t MAX_SPLITS = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t split_rsrc(const float *part, uint32_t splits, uint64_t stride) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(part), (short)0, (int)(4 * splits * stride), 0x00020000);
+}
+// Elements at byte offset `off` of split 0; splits are `sb` bytes apart.
+template <uint32_t S>
+__device__ __forceinline__ float split_sum(__amdgpu_buffer_rsrc_t r, uint32_t splits, uint32_t sb, uint32_t off) {
+  float p[S];
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) p[z] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off + z * sb, 0, 0));
+  float a = 0.f;
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) a = z < splits ? a + p[z] : a;
+  return a;
+}
+template <uint32_t S>
+__device__ __forceinline__ float4 split_sum4(__amdgpu_buffer_rsrc_t r, uint32_t splits, uint32_t sb, uint32_t off) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  u4 p[S];
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) p[z] = __builtin_amdgcn_raw_buffer_load_b128(r, off + z * sb, 0, 0);
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (uint32_t z = 0; z < S; z++) {
+    const bool in = z < splits;
+    a.x = in ? a.x + __uint_as_float(p[z].x) : a.x;
+    a.y = in ? a.y + __uint_as_float(p[z].y) : a.y;
+    a.z = in ? a.z + __uint_as_float(p[z].z) : a.z;
+    a.w = in ? a.w + __uint_as_float(p[z].w) : a.w;
+  }
+  return a;
+}
+
 // ------------------------------------------------------------------ argmax keys
 // Key = (order-preserving bits of the value) << 32 | (~index): the largest key is the
 // largest finite value with the lowest index. Non-finite entries never produce a key, so

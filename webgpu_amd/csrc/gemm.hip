@@ -517,11 +517,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemm a) {
 
 // Sum of the split-K partials part[z][tok][rows_total] in split order into each job's rows
 // (accumulate: added to y).
+template <uint32_t S>
 __global__ __launch_bounds__(256) void k_gemm_reduce(QGemm a, uint32_t splits) {
   const uint64_t n = (uint64_t)a.rows_total * a.batch;
+  const __amdgpu_buffer_rsrc_t rp = split_rsrc(a.part, splits, n);
   for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
-    float v = 0.f;
-    for (uint32_t z = 0; z < splits; z++) v += a.part[(uint64_t)z * n + i];
+    const float v = split_sum<S>(rp, splits, (uint32_t)(4 * n), (uint32_t)(4 * i));
     const uint32_t tok = (uint32_t)(i / a.rows_total);
     uint32_t r = (uint32_t)(i % a.rows_total), j = 0;
     while (j + 1 < a.njobs && r >= a.job[j].rows) { r -= a.job[j].rows; j++; }
@@ -532,23 +533,20 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(QGemm a, uint32_t splits) {
 
 // gate (rows [0, R)) and up (rows [R, 2R)) from the split-K partials, then act(gate) * up
 // into y [batch][R] and its split form for the down GEMM: one thread per eight columns of a
-// token.
+// token. S >= splits.
+template <uint32_t S>
 __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t splits, uint32_t R, uint32_t batch,
                                                     float *y, uint16_t *xs, int act) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i >= batch * (R / 8)) return;
   const uint32_t tok = i / (R / 8), k = (i % (R / 8)) * 8;
   const uint64_t n = (uint64_t)2 * R * batch, row = (uint64_t)tok * 2 * R;
-  float g[8] = {0, 0, 0, 0, 0, 0, 0, 0}, u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (uint32_t z = 0; z < splits; z++) {
-    const float *pg = part + z * n + row + k, *pu = pg + R;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const float4 a = *(const float4 *)(pg + 4 * h), b = *(const float4 *)(pu + 4 * h);
-      g[4 * h] += a.x; g[4 * h + 1] += a.y; g[4 * h + 2] += a.z; g[4 * h + 3] += a.w;
-      u[4 * h] += b.x; u[4 * h + 1] += b.y; u[4 * h + 2] += b.z; u[4 * h + 3] += b.w;
-    }
-  }
+  const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, splits, n);
+  const uint32_t sb = (uint32_t)(4 * n), og = (uint32_t)(4 * (row + k)), ou = og + 4 * R;
+  const float4 g0 = split_sum4<S>(rp, splits, sb, og), g1 = split_sum4<S>(rp, splits, sb, og + 16);
+  const float4 u0 = split_sum4<S>(rp, splits, sb, ou), u1 = split_sum4<S>(rp, splits, sb, ou + 16);
+  const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) v[e] = glu_act(g[e], act) * u[e];
@@ -684,6 +682,9 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
   // the GLU finish and a kept group always reduce from the partials (a single split too)
   const bool partials = splits > 1 || g.glu_out || g.keep_partials;
   if (partials && (!scratch->p || (uint64_t)splits * batch * q.rows_total > scratch->floats)) return hipErrorInvalidValue;
+  // the finishes read the partials through 32-bit buffer offsets
+  if (partials && (splits > MAX_SPLITS || (uint64_t)splits * batch * q.rows_total * 4 >= (1ull << 31)))
+    return hipErrorInvalidValue;
   q.part = partials ? scratch->p : nullptr;
   const dim3 grid(tiles, (batch + QG_N - 1) / QG_N, splits);
   const int a = types[0], b = types[1];
@@ -701,8 +702,15 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
   WGD_HIP(hipGetLastError());
   if (g.glu_out) {
     const uint32_t R = g.job[0].w->rows, count = batch * (R / 8);
-    hipLaunchKernelGGL(k_glu_reduce, dim3((count + 255) / 256), dim3(256), 0, s, (const float *)q.part, splits, R, batch,
-                       g.glu_out, scratch->xs, g.glu_act);
+    const dim3 grid((count + 255) / 256);
+    const float *part = q.part;
+    if (splits <= 2)
+      hipLaunchKernelGGL(k_glu_reduce<2>, grid, dim3(256), 0, s, part, splits, R, batch, g.glu_out, scratch->xs, g.glu_act);
+    else if (splits <= 4)
+      hipLaunchKernelGGL(k_glu_reduce<4>, grid, dim3(256), 0, s, part, splits, R, batch, g.glu_out, scratch->xs, g.glu_act);
+    else
+      hipLaunchKernelGGL(k_glu_reduce<MAX_SPLITS>, grid, dim3(256), 0, s, part, splits, R, batch, g.glu_out, scratch->xs,
+                         g.glu_act);
     WGD_HIP(hipGetLastError());
     scratch->xs_of = g.glu_out; scratch->xs_cols = R; scratch->xs_batch = batch;
   } else if (g.keep_partials) {
@@ -711,7 +719,8 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
     const uint64_t n = (uint64_t)q.rows_total * batch;
     uint32_t blocks = (uint32_t)((n + 255) / 256);
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(256), 0, s, q, splits);
+    if (splits <= 4) hipLaunchKernelGGL(k_gemm_reduce<4>, dim3(blocks), dim3(256), 0, s, q, splits);
+    else hipLaunchKernelGGL(k_gemm_reduce<MAX_SPLITS>, dim3(blocks), dim3(256), 0, s, q, splits);
   }
   return hipGetLastError();
 }

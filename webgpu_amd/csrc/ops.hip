@@ -79,6 +79,7 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
   __shared__ float red[RN_T / 64];
   const uint32_t tok = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint64_t stride = (uint64_t)n * batch;
+  const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, splits, stride);
   float *sr = state + (uint64_t)tok * n;
   float v[RN_G][8];
   float ss = 0.f;
@@ -86,13 +87,9 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
   for (uint32_t gi = 0; gi < RN_G; gi++) {
     const uint32_t k = 8 * (tid + RN_T * gi);
     if (k >= n) break;  // uniform per thread
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-    const float *p = part + (uint64_t)tok * n + k;
-    for (uint32_t z = 0; z < splits; z++) {
-      const float4 pa = *(const float4 *)(p + z * stride), pb = *(const float4 *)(p + z * stride + 4);
-      a.x += pa.x; a.y += pa.y; a.z += pa.z; a.w += pa.w;
-      b.x += pb.x; b.y += pb.y; b.z += pb.z; b.w += pb.w;
-    }
+    const uint32_t off = 4 * (tok * n + k);
+    float4 a = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off);
+    float4 b = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off + 16);
     const float4 ha = *(const float4 *)(sr + k), hb = *(const float4 *)(sr + k + 4);
     a = make_float4(ha.x + a.x, ha.y + a.y, ha.z + a.z, ha.w + a.w);
     b = make_float4(hb.x + b.x, hb.y + b.y, hb.z + b.z, hb.w + b.w);
@@ -127,7 +124,8 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
 hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
                              uint16_t *xs, uint32_t n, float eps, uint32_t batch) {
   if (!batch) return hipSuccess;
-  if (n % SPLIT_K || n > RN_G * 8 * RN_T || !splits ||
+  if (n % SPLIT_K || n > RN_G * 8 * RN_T || !splits || splits > MAX_SPLITS ||
+      (uint64_t)splits * n * batch * 4 >= (1ull << 31) ||
       ((uintptr_t)part | (uintptr_t)state | (uintptr_t)w | (uintptr_t)y) % 16)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_reduce_norm_split, dim3(batch), dim3(RN_T), 0, s, part, splits, state, w, y, xs, n, batch, eps);
@@ -334,9 +332,9 @@ __global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
   const float *bias = kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv;
   const uint64_t n = (uint64_t)a.rows_total * a.batch, base = (uint64_t)tok * a.rows_total + (uint64_t)slot * hd;
   float *v = buf[wv];
+  const __amdgpu_buffer_rsrc_t rp = split_rsrc(a.part, a.splits, n);
   for (uint32_t d = lane; d < hd; d += 64) {
-    float acc = 0.f;
-    for (uint32_t z = 0; z < a.splits; z++) acc += a.part[z * n + base + d];
+    const float acc = split_sum<MAX_SPLITS>(rp, a.splits, (uint32_t)(4 * n), (uint32_t)(4 * (base + d)));
     v[d] = bias ? acc + bias[h * hd + d] : acc;
   }
   __builtin_amdgcn_wave_barrier();
@@ -373,7 +371,8 @@ __global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
 
 hipError_t qkv_finish(hipStream_t s, const QKVFinish &a) {
   if (!a.batch) return hipSuccess;
-  if (a.hd > 512 || a.rot > a.hd || a.rot % 2 || !a.capacity || !a.cs || (a.mode == 0 && (!a.qn || !a.kn)))
+  if (a.hd > 512 || a.rot > a.hd || a.rot % 2 || !a.capacity || !a.cs || (a.mode == 0 && (!a.qn || !a.kn)) ||
+      !a.splits || a.splits > MAX_SPLITS || (uint64_t)a.splits * a.rows_total * a.batch * 4 >= (1ull << 31))
     return hipErrorInvalidValue;
   const uint32_t items = a.batch * (a.heads + 2 * a.kvh);
   hipLaunchKernelGGL(k_qkv_finish, dim3((items + 3) / 4), dim3(256), 0, s, a);
