@@ -216,10 +216,12 @@ def test_attention_long_context_and_ring(gpu, context, start, batch, window, cap
 
 # Prompt batches (the matrix-core path for head_dim 64/128/256): causal from position 0,
 # a batch deep in the context, a ragged batch with one query head per KV head, a sliding
-# window shorter than the batch's key range, and a wrapped ring.
+# window shorter than the batch's key range, and a wrapped ring. The last two split the
+# keys 7 and 15 ways (the merge's 8- and 16-split forms; the others merge at most 4).
 @pytest.mark.parametrize("heads,kvh,hd,start,batch,window,capacity", [
     (32, 8, 128, 0, 128, 4096, 1024), (32, 8, 128, 384, 128, 4096, 1024), (8, 8, 64, 100, 37, 4096, 256),
-    (16, 2, 256, 50, 20, 24, 128), (8, 2, 128, 1000, 48, 200, 256), (6, 2, 64, 7, 131, 4096, 512)])
+    (16, 2, 256, 50, 20, 24, 128), (8, 2, 128, 1000, 48, 200, 256), (6, 2, 64, 7, 131, 4096, 512),
+    (4, 4, 64, 400, 16, 4096, 512), (4, 4, 64, 900, 16, 4096, 1024)])
 def test_prompt_attention_batches(gpu, heads, kvh, hd, start, batch, window, capacity):
     rng = np.random.default_rng(start + batch)
     q = rng.standard_normal(batch * heads * hd).astype(np.float32) * 2
