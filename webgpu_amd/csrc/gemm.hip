@@ -470,14 +470,19 @@ __device__ __forceinline__ void gemm_tile(const QGemm &a, const QJob &jb, uint32
         Ah[i] = *(const bf16x8 *)(wt + frag_at(0, wm * 4 + i, ks, 0, 0) + 8 * lane);
         Al[i] = *(const bf16x8 *)(wt + frag_at(1, wm * 4 + i, ks, 0, 0) + 8 * lane);
       }
+      // the three products of a tile are 16 MFMAs apart (every tile's first, then second, then third)
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[ks][j], Ah[i], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bl[ks][j], Ah[i], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[ks][j], Al[i], acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[ks][j], Ah[i], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bl[ks][j], Ah[i], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Bh[ks][j], Al[i], acc[i][j], 0, 0, 0);
     }
     __syncthreads();
   }
