@@ -54,17 +54,35 @@ PEAK_HBM = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mv_matvec_microbench.md")
 
 
+# The sources of the roofline kernel; the counter summary records their digest, so a line whose
+# traffic comes from a profile of another version of the kernel says so.
+KERNEL_SOURCES = [os.path.join(ROOT, "webgpu_amd", "csrc", f) for f in ("matvec.hip", "matvec.h", "decode.h")]
+
+
+def kernel_source_digest() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for path in KERNEL_SOURCES:
+        with open(path, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def profiled_traffic(type_name: str, shape: str):
-    """traffic_bytes line of the committed counter summary for this shape, or None."""
+    """(traffic_bytes of the committed counter summary for this shape or None, whether the
+    summary was taken of the current kernel sources)."""
+    traffic, digest = None, None
     try:
         with open(TRAFFIC_PROFILE) as fh:
             for line in fh:
                 f = line.split()
                 if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == type_name and f[2] == shape:
-                    return int(f[3])
+                    traffic = int(f[3])
+                if len(f) == 2 and f[0] == "kernel_source_sha256":
+                    digest = f[1]
     except OSError:
         pass
-    return None
+    return traffic, digest == kernel_source_digest()
 METRIC = "decode tok/s (1 GPU) + Q4_K matvec HBM GB/s as % of peak"
 
 # Workloads: the default (the headline) and the other shaped decoders, each with its prompt,
@@ -498,8 +516,11 @@ def main() -> None:
                                       int(m["shape"].split("x")[1])) for m in mv[:3]}
         gpu.dispose()
         head = mv[0]
+        traffic, current = profiled_traffic(head["type"], head["shape"])
         result["roofline"] = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                              "frac": head["frac"], "traffic": profiled_traffic(head["type"], head["shape"]),
+                              "frac": head["frac"], "traffic": traffic,
+                              "traffic_source": "counters of the current kernel sources" if current else
+                              "counters of an older version of matvec.hip (profile not regenerated)",
                               "kernel": f"k_matvec<Q4K> {head['shape']} (in x out), {head['bytes']} B per launch",
                               "mean_us": head["us"]}
         result["matvec"] = mv

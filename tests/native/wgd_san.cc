@@ -22,6 +22,8 @@
 #include "bundle.h"
 
 static int failures = 0;
+// stage markers go to stderr (unbuffered), so a run that is killed still shows where it was
+static void stage(const char *what) { std::fprintf(stderr, "wgd_san: stage %s\n", what); }
 #define CHECK(cond, ...)                                            \
   do {                                                              \
     if (!(cond)) {                                                  \
@@ -357,6 +359,7 @@ static int run_model(const char *path, const char *out) {
   wgd_model_config cfg;
   std::memcpy(&cfg, b.wgd_cfg, sizeof cfg);
   wgd_context *ctx = nullptr;
+  stage("create");
   if (wgd_create(0, 0, &ctx) != WGD_OK) { std::fprintf(stderr, "wgd_san: %s\n", wgd_last_error(nullptr)); bundle_free(&b); return 3; }
   wgd_model *m = nullptr, *early = nullptr;
   OK(wgd_model_create(ctx, &cfg, b.capacities, &early));
@@ -367,6 +370,7 @@ static int run_model(const char *path, const char *out) {
     FAILS(wgd_model_ready(early), WGD_E_INVALID);
     wgd_model_destroy(early);
   }
+  stage("tensors");
   OK(wgd_model_create(ctx, &cfg, b.capacities, &m));
   if (!m) { wgd_destroy(ctx); bundle_free(&b); return 3; }
   for (uint32_t i = 0; i < b.n_tensors; i++) {
@@ -383,7 +387,9 @@ static int run_model(const char *path, const char *out) {
       OK(wgd_model_tensor(m, t->name, t->type, (int32_t)t->n_dims, t->dims, t->data, t->bytes));
     }
   }
+  stage("ready");
   OK(wgd_model_ready(m));
+  stage("prompt");
   std::vector<float> logits(cfg.vocab);
   int32_t arg = -1;
   FAILS(wgd_model_forward(m, b.prompt, cfg.batch + 1, 0, nullptr, nullptr), WGD_E_INVALID);
@@ -400,6 +406,7 @@ static int run_model(const char *path, const char *out) {
   std::vector<int32_t> tokens(b.steps > 0 ? b.steps : 1);
   tokens[0] = arg;
   const int32_t n = (int32_t)b.n_prompt, steps = (int32_t)b.steps;
+  stage("decode");
   FAILS(wgd_model_decode(m, arg, n, cfg.context, tokens.data() + 1), WGD_E_INVALID);
   if (steps > 2) OK(wgd_model_decode(m, arg, n, steps - 2, tokens.data() + 1));
   if (steps > 1) OK(wgd_model_forward(m, &tokens[steps - 2], 1, n + steps - 2, logits.data(), &tokens[steps - 1]));
@@ -407,12 +414,14 @@ static int run_model(const char *path, const char *out) {
   if (!rc) rc = bundle_write(out, logits.data(), 4ull * cfg.vocab, "ab");
   CHECK(rc == 0, "writing %s", out);
   // sampled decode graph: runs, and repeats itself from the same state
+  stage("sampled decode");
   OK(wgd_model_sampling(m, 0.7, 20, 0.95, 42));
   std::vector<int32_t> s1(4), s2(4);
   OK(wgd_model_decode(m, arg, n, 4, s1.data()));
   OK(wgd_model_decode(m, arg, n, 4, s2.data()));
   CHECK(s1 == s2, "sampled decode from the same state differs");
   OK(wgd_model_sampling(m, 0.0, 40, 0.9, 0));
+  stage("destroy");
   wgd_model_destroy(m);
   OK(wgd_done(ctx));
   wgd_destroy(ctx);
@@ -421,9 +430,12 @@ static int run_model(const char *path, const char *out) {
 }
 
 int main(int argc, char **argv) {
+  std::setvbuf(stdout, nullptr, _IONBF, 0);
   if (argc == 2 && !std::strcmp(argv[1], "api")) {
+    stage("contexts and buffers");
     check_context_and_buffers();
     wgd_context *ctx = nullptr;
+    stage("kernels");
     if (wgd_create(0, 0, &ctx) != WGD_OK) { std::fprintf(stderr, "wgd_san: %s\n", wgd_last_error(nullptr)); return 3; }
     check_kernels(ctx);
     wgd_destroy(ctx);
@@ -436,5 +448,6 @@ int main(int argc, char **argv) {
   }
   if (failures) { std::fprintf(stderr, "wgd_san: %d checks failed\n", failures); return 1; }
   std::printf("wgd_san %s: ok\n", argv[1]);
+  stage("exit");
   return 0;
 }

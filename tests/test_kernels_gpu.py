@@ -401,3 +401,30 @@ def test_quantize_with_rms_norm_then_matvec(gpu, type_, rows, cols):
     near(gpu.read_f32(yb, rows + 3)[3:], want, 1e-4, f"normed matvec {type_}")
     for b in (wb, xb, nb, yb, qb):
         gpu.destroy(b)
+
+
+@pytest.mark.parametrize("type_,rows,cols,normed", [(Q4_K, 4096, 4096, True), (Q4_K, 1024, 14336, False),
+                                                    (Q6_K, 1024, 5376, True), (Q5_K, 2048, 4096, True),
+                                                    (Q8_0, 1024, 5376, True), (Q4_0, 512, 4096, True)])
+def test_every_launch_shape_gives_the_same_bits(gpu, type_, rows, cols, normed):
+    """The decode step keeps whichever launch shape its measurement finds fastest, so every shape
+    it may pick (rows per workgroup, pipeline depth; the K split fixed) must give the same bits.
+    Inputs with a pending RMSNorm are the case where a reduction could follow the workgroup."""
+    rng = np.random.default_rng(cols + rows)
+    w = GEN[type_](rng, rows * cols // QUANTS[type_]["block"])
+    x = (rng.standard_normal(cols) * 2).astype(np.float32)
+    nw = (1 + rng.uniform(-0.2, 0.2, cols)).astype(np.float32)
+    wb, xb, nb = gpu.upload_weights(type_, cols, rows, w), gpu.upload(x, "x"), gpu.upload(nw, "norm")
+    qb = gpu.quantized_buffer(cols)
+    gpu.quantize(xb, cols, qb, nb if normed else None, 1e-6)
+    cap = 96
+    yb = gpu.buffer(cap * rows * 4, "y per shape")
+    n = gpu.matvec_shapes(type_, wb, qb, yb, cols, rows, cap)
+    assert n >= 4, f"only {n} launch shapes"
+    y = gpu.read_f32(yb, n * rows).reshape(n, rows)
+    differ = [k for k in range(1, n) if not np.array_equal(y[k].view(np.uint32), y[0].view(np.uint32))]
+    assert not differ, f"launch shapes {differ} of {n} differ from the cost model's"
+    xn = orc.norm(x, nw, 1e-6).astype(np.float32) if normed else x
+    near(y[0], orc.matmul(type_, w, xn, cols, rows, rows, 0, 0, 1), 1e-4, f"matvec {type_}")
+    for b in (wb, xb, nb, yb, qb):
+        gpu.destroy(b)

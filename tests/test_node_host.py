@@ -61,8 +61,8 @@ def test_addon_exports_engine_surface():
 
 
 # One binding per C-ABI entry point of include/wgd.h (the measurement helpers
-# wgd_probe_read and wgd_model_attention_timing, and the wgd_last_error/size getters folded
-# into thrown errors aside).
+# wgd_probe_read, wgd_model_attention_timing and wgd_matvec_shapes, and the
+# wgd_last_error/size getters folded into thrown errors aside).
 NODE_EXPORTS = ["create", "destroy", "adapterName", "memory", "done", "modelCreate", "modelTensor", "modelReady",
                 "modelForward", "modelDecode", "modelSampling", "modelDestroy", "bufferCreate", "bufferDestroy",
                 "bufferSize", "uploadWeights", "write", "read", "copy", "clear", "matmul", "quantizedBytes",

@@ -7,6 +7,8 @@ nothing through the context, and reject sizes whose partials exceed the array. T
 a row, the second smaller, check that the array's leftover contents from the first call do
 not leak into the second.
 """
+import re
+
 import numpy as np
 import pytest
 
@@ -50,7 +52,13 @@ def test_noalloc_attention_matches_the_allocating_entry_point():
         limit = int(lib().wgd_attention_noalloc_limit())
         heads, kvh, hd, batch, cap = 64, 8, 512, 128, 4096
         per_split = batch * heads * (hd + 2)
-        assert 2 * per_split > limit
+        # head_dim 512 runs the generic kernel: 2-query blocks for groups of 8 heads, and keys
+        # split over about four workgroups per CU (attn_plan in attention.hip); one split
+        # needs no scratch at all
+        cus = int(re.search(r"(\d+) CUs", gpu.adapterName).group(1))
+        nsplit = cus * 4 // (kvh * (batch // 2))
+        if nsplit < 2 or nsplit * per_split <= limit:
+            pytest.skip(f"{cus} CUs give {nsplit} key splits, whose partials fit the static scratch")
         bufs, n = _case(gpu, rng, heads, kvh, hd, 3000, batch, 4096, cap)
         y = gpu.buffer(n * 4, "y")
         with pytest.raises(WgdError, match="static scratch holds"):

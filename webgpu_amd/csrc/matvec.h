@@ -136,7 +136,7 @@ bool mv_supported(const Matrix &w);
 bool mv_mixable(int a, int b);
 // Number of argmax keys a single-matrix MV_STORE launch of w writes to MVOut::arg_part.
 uint32_t mv_arg_entries(const Matrix &w);
-MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out);
+MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out, bool normed);
 // y[r] (op)= mul * sum_c W[r][c] x[c] (+ bias[r]) for each target; epilogue `epi`
 // (store, residual add, or act(W x) * (W1 x) for a gated pair). `out` re-quantizes the
 // result of a single-target launch.
@@ -148,6 +148,9 @@ hipError_t mv(hipStream_t s, const MVTarget *t, uint32_t n, const QXView &x, int
 // state. Signatures already measured, F16 matrices and argmax-key launches are left alone.
 hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t n, const QXView &x, int epi,
                    const MVOut *out = nullptr);
+// Runs one single-matrix store launch per launch shape mv_tune may choose for it (the cost
+// model's first), shape k writing y + k * rows; *count = shapes run (at most max_shapes).
+hipError_t mv_shapes(hipStream_t s, const Matrix &w, const QXView &x, float *y, uint32_t max_shapes, uint32_t *count);
 inline hipError_t mv(hipStream_t s, const Matrix &w, const Matrix *w1, const QXView &x, float *y, int epi,
                      const MVOut *out = nullptr) {
   MVTarget t; t.w = &w; t.w1 = w1; t.y = y;

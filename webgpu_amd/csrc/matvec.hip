@@ -323,17 +323,18 @@ __device__ __forceinline__ float finish_row(const MV &m, const MVSeg &g, uint32_
 
 // LDS (dynamic): [0, 256) zeros (the A operand reads of off-diagonal lanes) | digit planes p
 // at 256 + p * ke | per 16-element block {scale / 254^2, sum} (ke / 16 float pairs) | partial
-// sums [NS][RT][4 groups] (two sets for a gated pair) | 16 floats of reduction scratch.
+// sums [NS][RT][4 groups] (two sets for a gated pair) | for an input with a pending RMSNorm,
+// the per-block sums of squares (ke / 16 floats).
 constexpr uint32_t MV_ZERO = 256;
-struct LdsMap { uint32_t digits, sm, vals, vals1, red, bytes; };
-__host__ __device__ inline LdsMap lds_map(uint32_t ke, uint32_t ns, uint32_t rt, bool glu) {
+struct LdsMap { uint32_t digits, sm, vals, vals1, sq, bytes; };
+__host__ __device__ inline LdsMap lds_map(uint32_t ke, uint32_t ns, uint32_t rt, bool glu, bool normed) {
   LdsMap l;
   l.digits = MV_ZERO;
   l.sm = MV_ZERO + 3 * ke;
   l.vals = l.sm + 8 * (ke / 16);
   l.vals1 = l.vals + 16 * ns * rt;
-  l.red = l.vals1 + (glu ? 16 * ns * rt : 0);
-  l.bytes = l.red + 64;
+  l.sq = l.vals1 + (glu ? 16 * ns * rt : 0);
+  l.bytes = l.sq + (normed ? 4 * (ke / 16) : 0);
   return l;
 }
 
@@ -343,7 +344,7 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t s = wv % m.NS, rg = wv / m.NS;
-  const LdsMap L = lds_map(m.ke, m.NS, m.RT, GLU);
+  const LdsMap L = lds_map(m.ke, m.NS, m.RT, GLU, m.x.normed != 0);
   const Rsrc rw = make_rsrc(g.w, g.bytes);
   const Rsrc rw1 = make_rsrc(GLU ? g.w1 : g.w, g.bytes);
   const uint32_t row0 = t * m.RT, tile0 = row0 / 16;
@@ -412,23 +413,24 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
 #pragma unroll
       for (int p = 0; p < 3; p++) *(uint4 *)(lds + L.digits + p * m.ke + e) = xd[p][j];
   }
-  float ss = 0.f;
+  // the sums of squares go to LDS by block index, so the epilogue adds them in an order that
+  // does not depend on the workgroup's shape (every launch shape gives the same bits)
+  float *sq = (float *)(lds + L.sq);
+  const bool normed = m.x.normed != 0;
 #pragma unroll
   for (uint32_t j = 0; j < XB; j++) {
     const uint32_t i = tid + j * nt;
-    if (i < blocks) *(float2 *)(lds + L.sm + 8 * i) = make_float2(__uint_as_float(xsc[j]) * (1.f / 64516.f), __uint_as_float(xsm[j]));
-    ss += __uint_as_float(xsq[j]);
+    if (i < blocks) {
+      *(float2 *)(lds + L.sm + 8 * i) = make_float2(__uint_as_float(xsc[j]) * (1.f / 64516.f), __uint_as_float(xsm[j]));
+      if (normed) sq[i] = __uint_as_float(xsq[j]);
+    }
   }
   for (uint32_t e = (tid + XJ * nt) * 16; e < m.ke; e += nt * 16)
 #pragma unroll
     for (int p = 0; p < 3; p++) *(uint4 *)(lds + L.digits + p * m.ke + e) = bl16c(rxd[p], e);
   for (uint32_t i = tid + XB * nt; i < blocks; i += nt) {
     *(float2 *)(lds + L.sm + 8 * i) = make_float2(__uint_as_float(bl4c(rxs, 4 * i)) * (1.f / 64516.f), __uint_as_float(bl4c(rxm, 4 * i)));
-    ss += __uint_as_float(bl4c(rxq, 4 * i));
-  }
-  if (m.x.normed) {
-    ss = wave_sum(ss);
-    if (lane == 0) ((float *)(lds + L.red))[wv] = ss;
+    if (normed) sq[i] = __uint_as_float(bl4c(rxq, 4 * i));
   }
   __syncthreads();
   // per-lane LDS addresses of the A operands: diagonal lanes read digit p = r % 4 of their
@@ -496,11 +498,12 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   __syncthreads();
   if (threadIdx.x >= ((m.RT + 63) & ~63u)) return;
   float xm = 1.f;
-  if (m.x.normed) {
+  if (normed) {
+    // lane l adds blocks l, l + 64, ... in order, then the butterfly (all lanes get the same
+    // total): a fixed order for every launch shape
     float tot = 0.f;
-    const uint32_t nw = blockDim.x >> 6;
-    for (uint32_t k = 0; k < nw; k++) tot += ((const float *)(lds + L.red))[k];
-    xm = 1.f / sqrtf(tot / (float)m.x.len + m.x.eps);
+    for (uint32_t i = lane; i < blocks; i += 64) tot += sq[i];
+    xm = 1.f / sqrtf(wave_sum(tot) / (float)m.x.len + m.x.eps);
   }
   const uint32_t row = threadIdx.x;
   const bool inside = row < m.RT && row0 + row < g.rows;
@@ -741,7 +744,7 @@ bool mv_mixable(int a, int b) {
 static uint32_t lds_limit() { return LDS_MAX; }
 
 uint32_t mv_arg_entries(const Matrix &w) {
-  const MVPlan p = mv_plan(w, &w.rows, 1, false, false);
+  const MVPlan p = mv_plan(w, &w.rows, 1, false, false, true);
   return p.tiles * ((p.RT + 63) / 64);
 }
 
@@ -751,7 +754,7 @@ uint32_t mv_arg_entries(const Matrix &w) {
 // stretched when a CU holds less than ~64 KB of weight loads in flight (more than ~100 KB
 // only queues), when the activation staging is amortised over few rows, and for idle chunk
 // columns.
-MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out) {
+MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool quantized_out, bool normed) {
   if (float_type(w.type)) return mv16_plan(w, rows, n);
   MVPlan best_p{};
   const uint32_t N = chunk_elems(w.type), C = w.cols / N, CQ = (C + 7) / 8;
@@ -771,7 +774,7 @@ MVPlan mv_plan(const Matrix &w, const uint32_t *rows, uint32_t n, bool glu, bool
         const uint32_t rt = 16 * nr * iter;
         if (rt > 64 * nr * ns || rt > 1024) break;  // one epilogue thread per row
         if (quantized_out && rt % 16) continue;
-        const LdsMap lm = lds_map(ke, ns, rt, glu);
+        const LdsMap lm = lds_map(ke, ns, rt, glu, normed);
         if (lm.bytes > lds_limit()) break;
         const uint32_t units = iter * nsb;
         uint32_t tiles = 0;
@@ -857,28 +860,22 @@ __global__ void k_hold(long long ticks) {
 // the same bits) and vary the rows per workgroup (NR groups of ITER steps) and the pipeline
 // depth DU. Each is timed with HIP events over back-to-back launches that rotate through the
 // sets (so the weights come from HBM, not a cache); the fastest is kept for the signature.
-hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t n, const QXView &x, int epi,
-                   const MVOut *out) {
-  if (!nsets || n < 1 || n > (uint32_t)MV_MAX_SEGS) return hipErrorInvalidValue;
-  const Matrix &w0 = *sets[0].w;
-  if (float_type(w0.type) || (out && out->arg_part)) return hipSuccess;  // F16/F32 and the head keep the model's plan
-  const bool glu = sets[0].w1 != nullptr, qout = out && out->q.d0;
-  const PlanKey key = plan_key(sets, n, epi, qout);
-  {
-    std::lock_guard<std::mutex> lock(g_plan_mu);
-    if (g_plans.count(key)) return hipSuccess;
-  }
+// The launch shapes mv_tune times for one signature: the cost model's plan first, then every
+// other (NR, ITER, DU) with the model's K split.
+static std::vector<MVPlan> mv_candidates(const MVTarget *t, uint32_t n, const QXView &x, bool qout) {
+  const Matrix &w0 = *t[0].w;
+  const bool glu = t[0].w1 != nullptr;
   uint32_t rows[MV_MAX_SEGS];
-  for (uint32_t i = 0; i < n; i++) rows[i] = sets[i].w->rows;
-  const MVPlan base = mv_plan(w0, rows, n, glu, qout);
-  if (!base.RT) return hipErrorInvalidValue;
+  for (uint32_t i = 0; i < n; i++) rows[i] = t[i].w->rows;
+  const MVPlan base = mv_plan(w0, rows, n, glu, qout, x.normed != 0);
+  if (!base.RT) return {};
   const uint32_t ke = base.NS * base.NSB * 8 * chunk_elems(w0.type);
   std::vector<MVPlan> cands{base};
   for (uint32_t nr = 1; nr * base.NS <= 16; nr++)
     for (uint32_t it = 1; it <= 8; it++) {
       const uint32_t rt = 16 * nr * it;
       if (rt > 64 * nr * base.NS || rt > 1024) break;
-      const uint32_t lds = lds_map(ke, base.NS, rt, glu).bytes;
+      const uint32_t lds = lds_map(ke, base.NS, rt, glu, x.normed != 0).bytes;
       if (lds > lds_limit()) break;
       uint32_t tiles = 0;
       for (uint32_t i = 0; i < n; i++) tiles += (rows[i] + rt - 1) / rt;
@@ -890,6 +887,35 @@ hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t
         if (p.NR != base.NR || p.ITER != base.ITER || p.DU != base.DU) cands.push_back(p);
       }
     }
+  return cands;
+}
+
+hipError_t mv_shapes(hipStream_t s, const Matrix &w, const QXView &x, float *y, uint32_t max_shapes, uint32_t *count) {
+  MVTarget t; t.w = &w; t.w1 = nullptr; t.y = y;
+  const std::vector<MVPlan> cands = float_type(w.type) ? std::vector<MVPlan>{} : mv_candidates(&t, 1, x, false);
+  *count = (uint32_t)std::min<size_t>(cands.size(), max_shapes);
+  for (uint32_t k = 0; k < *count; k++) {
+    t.y = y + (uint64_t)k * w.rows;
+    const hipError_t e = mv_launch(s, &t, 1, x, MV_STORE, nullptr, &cands[k]);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t mv_tune(hipStream_t s, const MVTarget *sets, uint32_t nsets, uint32_t n, const QXView &x, int epi,
+                   const MVOut *out) {
+  if (!nsets || n < 1 || n > (uint32_t)MV_MAX_SEGS) return hipErrorInvalidValue;
+  const Matrix &w0 = *sets[0].w;
+  if (float_type(w0.type) || (out && out->arg_part)) return hipSuccess;  // F16/F32 and the head keep the model's plan
+  const bool qout = out && out->q.d0;
+  const PlanKey key = plan_key(sets, n, epi, qout);
+  {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    if (g_plans.count(key)) return hipSuccess;
+  }
+  const std::vector<MVPlan> cands = mv_candidates(sets, n, x, qout);
+  if (cands.empty()) return hipErrorInvalidValue;
+  const MVPlan &base = cands[0];
   hipEvent_t e0 = nullptr, e1 = nullptr;
   WGD_HIP(hipEventCreate(&e0));
   hipError_t err = hipEventCreate(&e1);
@@ -1001,7 +1027,7 @@ static hipError_t mv_launch(hipStream_t s, const MVTarget *t, uint32_t n, const 
     const auto it = g_plans.find(plan_key(t, n, epi, qout));
     if (it != g_plans.end()) p = it->second;
   }
-  if (!p.RT) p = mv_plan(w0, rows, n, glu, qout);
+  if (!p.RT) p = mv_plan(w0, rows, n, glu, qout, x.normed != 0);
   if (!p.RT || p.threads != 64 * p.NS * p.NR || p.threads > 1024 || p.RT > p.threads || p.NSB % p.DU ||
       p.lds > lds_limit() || (qout && p.RT % 16))
     return hipErrorInvalidValue;

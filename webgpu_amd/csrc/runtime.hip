@@ -117,7 +117,9 @@ int wgd_create(int32_t device, uint64_t budget_bytes, wgd_context **out) {
   size_t free_b = 0, total_b = 0;
   hipMemGetInfo(&free_b, &total_b);
   ctx->limit = budget_bytes ? budget_bytes : (uint64_t)free_b;
-  ctx->adapter = std::string(p.name) + " (" + p.gcnArchName + ", " + std::to_string(p.multiProcessorCount) + " CUs)";
+  // the marketing name can be empty (a driver that does not report it): name the device by index then
+  const std::string name = p.name[0] ? std::string(p.name) : "HIP device " + std::to_string(device);
+  ctx->adapter = name + " (" + p.gcnArchName + ", " + std::to_string(p.multiProcessorCount) + " CUs)";
   void *scratch = nullptr;
   if (ctx_alloc(ctx, 8 + 8 * 256, "argmax scratch", &scratch) != WGD_OK) {
     g_error = ctx->error;
@@ -347,6 +349,24 @@ int wgd_matvec(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
   if (qx->qx_cols != cols) return fail(ctx, WGD_E_INVALID, "matvec: %s holds no quantized row of %u columns (wgd_quantize first)", qx->label.c_str(), cols);
   const QXView xv = qx_const(qx_view(qx->ptr, cols), cols, qx->qx_normed, qx->qx_eps);
   return ctx_check(ctx, mv(ctx->stream, m, nullptr, xv, (float *)y->ptr + row_base, MV_STORE), "matvec");
+}
+
+int wgd_matvec_shapes(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *qx, wgd_buffer *y,
+                      uint32_t cols, uint32_t rows, uint32_t max_shapes, uint32_t *count) {
+  NEED_CTX(ctx); NEED_BUF(ctx, w, "matvec_shapes"); NEED_BUF(ctx, qx, "matvec_shapes"); NEED_BUF(ctx, y, "matvec_shapes");
+  if (!count) return fail(ctx, WGD_E_INVALID, "matvec_shapes: NULL count");
+  *count = 0;
+  if (!known_type(type) || !cols || !rows || cols % block_size(type)) return fail(ctx, WGD_E_INVALID, "matvec_shapes: type %d, %ux%u", type, cols, rows);
+  NEED_FIT(ctx, w, (uint64_t)rows * row_bytes(type, cols), "matvec weights");
+  NEED_FIT(ctx, qx, qx_bytes(cols), "quantized activation");
+  NEED_FIT(ctx, y, (uint64_t)max_shapes * rows * 4, "matvec_shapes output");
+  Matrix m; m.data = (const uint8_t *)w->ptr; m.type = type; m.layout = w->layout; m.cols = cols; m.rows = rows;
+  if (w->layout != LAYOUT_GGUF && (w->type != type || w->cols != cols || w->rows != rows))
+    return fail(ctx, WGD_E_INVALID, "matvec_shapes: weights %s were uploaded as type %d, %ux%u", w->label.c_str(), w->type, w->cols, w->rows);
+  if (!mv_supported(m)) return fail(ctx, WGD_E_INVALID, "matvec_shapes: type %d in this layout has no quantized matvec", type);
+  if (qx->qx_cols != cols) return fail(ctx, WGD_E_INVALID, "matvec_shapes: %s holds no quantized row of %u columns", qx->label.c_str(), cols);
+  const QXView xv = qx_const(qx_view(qx->ptr, cols), cols, qx->qx_normed, qx->qx_eps);
+  return ctx_check(ctx, mv_shapes(ctx->stream, m, xv, (float *)y->ptr, max_shapes, count), "matvec_shapes");
 }
 
 int wgd_dequant(wgd_context *ctx, int32_t type, const wgd_buffer *w, wgd_buffer *out, uint64_t count) {

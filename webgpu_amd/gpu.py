@@ -43,6 +43,7 @@ SIGNATURES = {
     "wgd_quantized_bytes": (_U64, [_U32]),
     "wgd_quantize": (C.c_int, [_P, _P, _U32, _P, _F, _P]),
     "wgd_matvec": (C.c_int, [_P, _I32, _P, _P, _P, _U32, _U32, _U32]),
+    "wgd_matvec_shapes": (C.c_int, [_P, _I32, _P, _P, _P, _U32, _U32, _U32, C.POINTER(_U32)]),
     "wgd_norm": (C.c_int, [_P, _P, _P, _P, _U32, _F, _U32]),
     "wgd_rope_norm": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _F, _F, _F, _U32, _U32]),
     "wgd_rope_neox": (C.c_int, [_P, _P, _U32, _U32, _U32, _F, _F, _U32, _U32]),
@@ -223,6 +224,14 @@ class Compute:
 
     def matvec(self, type_: int, w: Buffer, qx: Buffer, y: Buffer, cols: int, rows: int, row_base: int = 0) -> None:
         self.check(lib().wgd_matvec(self.ctx, type_, w.ptr, qx.ptr, y.ptr, cols, rows, row_base))
+
+    def matvec_shapes(self, type_: int, w: Buffer, qx: Buffer, y: Buffer, cols: int, rows: int,
+                      max_shapes: int) -> int:
+        """wgd_matvec once per launch shape the decode step's measurement may pick; returns the
+        number of shapes run (shape k wrote y[k * rows:(k + 1) * rows])."""
+        n = C.c_uint32(0)
+        self.check(lib().wgd_matvec_shapes(self.ctx, type_, w.ptr, qx.ptr, y.ptr, cols, rows, max_shapes, C.byref(n)))
+        return n.value
 
     def dequant(self, type_: int, w: Buffer, out: Buffer, count: int) -> None:
         self.check(lib().wgd_dequant(self.ctx, type_, w.ptr, out.ptr, count))
