@@ -141,7 +141,7 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 def load_fixture(name):
     import xxhash
     z = np.load(os.path.join(GOLDEN, f"model_{name}.npz"), allow_pickle=False)
-    f = synth.build(name)
+    f = synth.build(str(z["model"]))
     assert xxhash.xxh64(memoryview(f)).hexdigest() == str(z["gguf_xxh64"]), \
         f"{name}: the synthetic GGUF differs from the one the fixture was made from"
     return f, z
@@ -213,6 +213,20 @@ def test_gemma3_full_width_local_rings_wrap():
 
 
 @pytest.mark.slow
+def test_gemma3_27b_widths_8k_prompt_global_layer():
+    """The Gemma-3-27B workload's own prompt, 8192 tokens in 64 batches of 128, at full width
+    over six layers (five local, one global), then 48 free-running greedy tokens: the global
+    layer's attention reads every prompt key through the split-K decode kernel, against the
+    oracle's fixture."""
+    eng, z = run_workload("gemma3-27b-6l-8k")
+    try:
+        assert max(eng.kvCapacities) == int(z["context"]) == 8448 and int(z["prompt_len"]) == 8192
+        assert min(eng.kvCapacities) == 1151
+    finally:
+        eng.dispose()
+
+
+@pytest.mark.slow
 def test_gemma3_27b_shape_local_and_global_layers():
     """All 62 layers against the oracle at a short prompt (logits and tokens)."""
     eng, *_ = check_model("gemma3-27b", 24, 3, context=2048)
@@ -221,9 +235,9 @@ def test_gemma3_27b_shape_local_and_global_layers():
 
 @pytest.mark.slow
 def test_gemma3_27b_8k_context_properties():
-    """All 62 layers at the 8192-token prompt of the Gemma workload (64 batches of 128): the
-    logits are finite, the graph decode loop equals eager steps for 16 tokens, and a replay
-    from the same state repeats them."""
+    """All 62 layers at the Gemma workload itself (the 8192-token prompt in 64 batches of 128,
+    then its 128 decode tokens): the logits are finite, the graph decode loop equals eager
+    steps for all 128 tokens, and a replay from the same state repeats them."""
     f, g, c, caps, eng = build("gemma3-27b", 8448)
     try:
         ids = synth.prompt_ids(c.vocab, 8192, 7)
@@ -231,13 +245,13 @@ def test_gemma3_27b_8k_context_properties():
             logits = eng.forward(ids[i:i + 128], i, i + 128 == 8192)
         assert np.isfinite(logits).all()
         first = int(np.argmax(logits))
-        dev = eng.decode(first, 8192, 16)
+        dev = eng.decode(first, 8192, 128)
         eager, tok = [], first
-        for i in range(16):
+        for i in range(128):
             tok = eng.forward_argmax([tok], 8192 + i)
             eager.append(tok)
         assert dev == eager
-        assert eng.decode(first, 8192, 16) == dev
+        assert eng.decode(first, 8192, 128) == dev
         print(f"\ngemma3-27b 8K: tokens {dev}", flush=True)
     finally:
         eng.dispose()

@@ -368,3 +368,22 @@ def test_sample_closed_forms():
     assert np.abs(got - probs / probs.sum()).max() < 2e-4
     with pytest.raises(ValueError):
         orc.sample(np.array([np.nan, np.inf], np.float32), 0.7, 40, 0.9, 0.5)
+
+
+# ---------------------------------------------------------------- the whole-workload fixtures
+# name -> least distinct greedy tokens: a free-running run that repeats one token checks a
+# fixed point, not the state the model carries from step to step
+FIXTURE_DYNAMICS = {"qwen3-0.6b": 64, "gemma3-27b-6l": 24, "gemma3-27b-6l-8k": 36, "llama3-8b": 200}
+
+
+@pytest.mark.parametrize("name", sorted(FIXTURE_DYNAMICS))
+def test_model_fixtures_run_through_varied_tokens_with_clear_margins(name):
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"model_{name}.npz"),
+                allow_pickle=False)
+    toks = z["tokens"].tolist()
+    assert len(toks) == int(z["steps"]) and len(z["prompt"]) == int(z["prompt_len"])
+    assert len(set(toks)) >= FIXTURE_DYNAMICS[name], f"{name}: {len(set(toks))} distinct tokens in {len(toks)}"
+    # every step's oracle top-2 margin clears the logits tolerance, so identical tokens are a fair demand
+    assert (z["margins"] >= 1e-3 * z["maxabs"]).all()
+    assert int(np.argmax(z["first_logits"])) == toks[0] and int(np.argmax(z["last_logits"])) == toks[-1]

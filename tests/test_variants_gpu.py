@@ -2,8 +2,10 @@
 float64 oracle: two prompt batches (the planar-weight GEMM path with its fused Q/K/V,
 GLU and residual finishes, or its per-matrix fallback) then greedy decode steps on the
 quantized matvec path. Same contract as the shaped decoders: logits within 1e-3
-max-relative error, greedy tokens identical (or a top-2 margin below the tolerance),
-teacher-forced on the oracle's tokens.
+max-relative error and greedy tokens identical, with no exception for small margins. The
+prompt seed is the first from 3 whose oracle steps all have a top-2 margin of at least the
+logits tolerance (1e-3 max|logit|), the rule the whole-workload fixtures follow, so an
+identical token is a fair demand at every step.
 """
 import numpy as np
 import pytest
@@ -22,39 +24,58 @@ def max_rel(got, want):
     return float(np.abs(np.asarray(got, np.float64) - want).max() / np.abs(want).max())
 
 
+def oracle_run(f, g, c, context, caps, batch, seed, steps):
+    """The oracle's prompt (batches of `batch`) and greedy steps for one prompt seed: the ids,
+    the logits after the prompt and after each step, the tokens and the smallest top-2 margin
+    relative to max|logit|."""
+    ora = orc.OracleModel(f, g, c, context, caps)
+    try:
+        ids = synth.prompt_ids(c.vocab, 100, seed=seed)
+        for i in range(0, len(ids), batch):  # batches of 64 and 36 tokens
+            part = ids[i:i + batch]
+            want = ora.forward(part, i, logits=i + len(part) == len(ids))
+        logits, toks, worst, pos = [want], [], np.inf, len(ids)
+        for s in range(steps):
+            order = np.argsort(-want, kind="stable")
+            toks.append(int(order[0]))
+            worst = min(worst, float(want[order[0]] - want[order[1]]) / float(np.abs(want).max()))
+            if s + 1 < steps:
+                want = ora.forward([toks[-1]], pos)
+                logits.append(want)
+                pos += 1
+        return ids, logits, toks, worst
+    finally:
+        ora.close()
+
+
 @pytest.mark.parametrize("kind", qvariants.KINDS)
 def test_quantized_variant_prefill_and_decode(kind):
     f, g, c = qvariants.build(kind)
-    context, batch = 256, 64
+    context, batch, steps = 256, 64, 5
     caps = attention_memory(c, context, batch)["capacities"]
+    for seed in range(3, 40):
+        ids, wants, toks, worst = oracle_run(f, g, c, context, caps, batch, seed, steps)
+        if worst >= LOGIT_TOL:
+            break
+    assert worst >= LOGIT_TOL, f"{kind}: no prompt seed in 3-39 whose oracle margins clear the tolerance"
     eng = PagedEngine()
     eng.load(f, LoadOptions(contextLength=context, batchSize=batch))
-    ora = orc.OracleModel(f, g, c, context, caps)
     try:
-        ids = synth.prompt_ids(c.vocab, 100, seed=3)
-        errs = []
-        want = got = None
-        for i in range(0, len(ids), batch):  # batches of 64 and 36 tokens
+        for i in range(0, len(ids), batch):
             part = ids[i:i + batch]
-            last = i + len(part) == len(ids)
-            want = ora.forward(part, i, logits=last)
-            got = eng.forward(part, i, last)
-        errs.append(max_rel(got, want))
-        pos = len(ids)
-        for s in range(4):
-            order = np.argsort(-want, kind="stable")
-            tok = int(order[0])
-            margin = float(want[order[0]] - want[order[1]])
-            assert int(np.argmax(got)) == tok or margin < LOGIT_TOL * np.abs(want).max(), \
-                f"{kind} step {s}: GPU token {int(np.argmax(got))} vs oracle {tok} (margin {margin:.3e})"
-            want = ora.forward([tok], pos)
-            got = eng.forward([tok], pos, True)
-            errs.append(max_rel(got, want))
-            pos += 1
-        print(f"\n{kind}: max-rel logits error {max(errs):.3e}")
+            got = eng.forward(part, i, i + len(part) == len(ids))
+        errs, pos = [], len(ids)
+        for s in range(steps):
+            errs.append(max_rel(got, wants[s]))
+            assert int(np.argmax(got)) == toks[s], \
+                f"{kind} seed {seed} step {s}: GPU token {int(np.argmax(got))} vs oracle {toks[s]}"
+            if s + 1 < steps:
+                got = eng.forward([toks[s]], pos, True)
+                pos += 1
+        print(f"\n{kind}: prompt seed {seed}, min oracle margin {worst:.2e} of max|logit|, "
+              f"max-rel logits error {max(errs):.3e}, tokens {toks}")
         assert max(errs) <= LOGIT_TOL, f"{kind}: logits max-rel error {max(errs):.3e}"
     finally:
-        ora.close()
         eng.dispose()
 
 

@@ -18,6 +18,15 @@ sub-block (E[sc*q] = 7.5 E[m] * sc-mean), and d sized so the weights have std ~0
 Q6_K blocks get uniform quants and int8 scales with d sized the same way (often an f16
 subnormal, which the decode must and does handle). Norm vectors are 1 + U(-0.1, 0.1) as
 the reference's ``eins`` (verify-dense.mjs:74).
+
+Tied heads: where ``token_embd`` is also the output matrix, logit j is the normed state
+dotted with w * e_j, and with all-positive output-norm weights the current token's own
+embedding (a large share of the state at Gemma's sqrt(hidden) input scale) scores itself
+highest, so greedy decoding repeats one token forever. ``signed_out_norm`` draws the
+output-norm entries with random signs, which takes that self-affinity to zero mean; the
+Qwen3-0.6B shape also draws its embeddings at std 1 (``embd_std``), so the current token,
+not the context average, sets the next one. Both are choices of random initialisation
+only: the tensor directory, types and shapes are unchanged.
 """
 from __future__ import annotations
 
@@ -148,6 +157,8 @@ class Spec:
     std: float = 0.02
     norm_ones: bool = False         # norm vectors exactly 1 (tiny) instead of 1 + U(-0.1, 0.1)
     seed: int = 1234
+    embd_std: Optional[float] = None  # token_embd std (default: std)
+    signed_out_norm: bool = False     # output_norm entries carry random signs
 
 
 SPECS: Dict[str, Spec] = {
@@ -155,7 +166,8 @@ SPECS: Dict[str, Spec] = {
                  {"embd": F32, "output": F32, "attn": F32, "v": F32, "ffn": F32}, norm_ones=True, seed=13,
                  context_length=2048),
     "qwen3-0.6b": Spec("qwen3-0.6b", "qwen3", 28, 1024, 16, 8, 128, 3072, 151936, 1e-6, 1_000_000.0, True, True,
-                       {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K}, context_length=40960),
+                       {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K}, context_length=40960,
+                       embd_std=1.0, signed_out_norm=True),
     "llama3-8b": Spec("llama3-8b", "llama", 32, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500_000.0, False, False,
                       {"embd": Q4_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K}, context_length=8192),
     "gemma3-27b": Spec("gemma3-27b", "gemma3", 62, 5376, 32, 16, 128, 21504, 262144, 1e-6, 1_000_000.0, True, True,
@@ -165,7 +177,7 @@ SPECS: Dict[str, Spec] = {
     # this depth modelConfig takes the attention scale 1/sqrt(head_dim) (gguf.ts:134).
     "gemma3-27b-6l": Spec("gemma3-27b-6l", "gemma3", 6, 5376, 32, 16, 128, 21504, 262144, 1e-6, 1_000_000.0, True,
                           True, {"embd": Q6_K, "output": Q6_K, "attn": Q4_K, "v": Q6_K, "ffn": Q4_K},
-                          context_length=131072),
+                          context_length=131072, signed_out_norm=True),
     # Small quantized models for the sanitizer runs: every weight type, both rope modes, a
     # Gemma-3 layer period of six with 16-token local windows (a 40-token prompt in 8-token
     # batches wraps their rings) and head dims off the 64/128/256 fast paths.
@@ -287,19 +299,22 @@ def build(spec: Spec | str, seed: Optional[int] = None) -> np.ndarray:
         n = int(np.prod(dims))
         dst = f[data_start + o: data_start + o + tensor_bytes(dims, typ)]
         tseed = (seed * 1_000_003 + i * 7919) & 0x7FFFFFFF
+        std = s.embd_std if role == "embd" and s.embd_std is not None else s.std
         if role == "norm":
             if s.norm_ones:
                 v = np.ones(n, np.float32)
             else:
                 v = (1.0 + np.random.default_rng(tseed).uniform(-0.1, 0.1, n)).astype(np.float32)
+            if s.signed_out_norm and name == "output_norm.weight":
+                v *= np.where(np.random.default_rng(tseed + 1).integers(0, 2, n) == 1, 1.0, -1.0).astype(np.float32)
             dst[:] = v.view(np.uint8)
         elif typ == F32:
-            dst[:] = lcg_normal(tseed, n, s.std).view(np.uint8)
+            dst[:] = lcg_normal(tseed, n, std).view(np.uint8)
         else:
             rng = np.random.default_rng(tseed)
             nb = n // QUANTS[typ]["block"]
             gen = {Q4_K: q4k_blocks, Q6_K: q6k_blocks, Q8_0: q8_0_blocks}[typ]
-            dst[:] = gen(rng, nb, s.std)
+            dst[:] = gen(rng, nb, std)
     return f
 
 
