@@ -499,11 +499,14 @@ __device__ __forceinline__ void mv_tile(const MV &m, const MVSeg &g, uint32_t t,
   if (threadIdx.x >= ((m.RT + 63) & ~63u)) return;
   float xm = 1.f;
   if (normed) {
-    // lane l adds blocks l, l + 64, ... in order, then the butterfly (all lanes get the same
-    // total): a fixed order for every launch shape
+    // lane l adds blocks 4l .. 4l + 3 (then 256 further on), and the DPP fold adds the lanes:
+    // a fixed order for every launch shape (blocks is a multiple of 8)
     float tot = 0.f;
-    for (uint32_t i = lane; i < blocks; i += 64) tot += sq[i];
-    xm = 1.f / sqrtf(wave_sum(tot) / (float)m.x.len + m.x.eps);
+    for (uint32_t i = 4 * lane; i < blocks; i += 256) {
+      const float4 q = *(const float4 *)(sq + i);
+      tot += (q.x + q.y) + (q.z + q.w);
+    }
+    xm = 1.f / sqrtf(wave_total(tot) / (float)m.x.len + m.x.eps);
   }
   const uint32_t row = threadIdx.x;
   const bool inside = row < m.RT && row0 + row < g.rows;
