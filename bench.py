@@ -303,6 +303,30 @@ def trace_summary(directory: str) -> None:
         print(f"| `{k}` | {g} | {len(v) / ntok:.2f} | {sum(v) / len(v):.2f} | {sum(v) / ntok:.1f} | {100 * sum(v) / tot:.1f}% |")
 
 
+def attention_timings(eng, a, spec, context: int, pos: int):
+    """Decode attention alone (one layer's launch pair, HIP events over 50 launches), at the
+    middle and the end of the timed window; Gemma-3 at a local (sliding) and a global layer.
+    Bytes: the K and V rows of every attended key (min(pos + 1, window) keys x kv_heads x
+    head_dim x 2)."""
+    attn = []
+    esz = 2 if a.kv == "f16" else 4
+    cfg = eng.config
+    gemma = cfg.family == "gemma3"
+    layers = [0, cfg.period - 1] if gemma else [0]
+    for layer in layers:
+        window = cfg.window if gemma and layer % cfg.period != cfg.period - 1 else context
+        for p in sorted({pos + a.steps // 2, pos + a.steps}):
+            if p >= context:
+                continue
+            us = eng.attention_timing(layer, p, 50)
+            nbytes = min(p + 1, window) * spec.kv_heads * spec.head_dim * 2 * esz
+            attn.append({"layer": layer, "pos": p, "keys": min(p + 1, window), "us": us, "bytes": nbytes,
+                         "GBps": nbytes / us / 1e3, "frac": nbytes / us / 1e3 / (PEAK_HBM / 1e9)})
+            print(f"[bench] decode attention layer {layer} at position {p}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s "
+                  f"({100 * nbytes / us / 1e3 / (PEAK_HBM / 1e9):.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+    return attn
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -325,6 +349,9 @@ def main() -> None:
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the matvec microbench and a 256 MiB device copy (counter calibration), no JSON line")
     ap.add_argument("--gemm-only", action="store_true", help="only the prompt-GEMM microbench, no JSON line")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="load and prefill the model, then only the decode attention timings (and a 256 MiB device "
+                         "copy for counter calibration), no JSON line")
     ap.add_argument("--probe", action="store_true",
                     help="only the plain-read probe (the per-launch read floor) at the matvec byte counts, with and "
                          "without a result store; one JSON line per case")
@@ -427,6 +454,17 @@ def main() -> None:
         eng.gpu.done()
         return time.perf_counter() - t, tok
     prefill()
+    if a.attention_only:
+        n = 256 << 20  # a plain copy of known size: its counters per dispatch scale the attention's
+        src, dst = eng.gpu.buffer(n, "copy src"), eng.gpu.buffer(n, "copy dst")
+        for _ in range(4):
+            eng.gpu.copy(src, dst, n)
+        eng.gpu.done()
+        eng.gpu.destroy(src)
+        eng.gpu.destroy(dst)
+        attention_timings(eng, a, spec, context, a.prompt)
+        eng.dispose()
+        return
     runs = [prefill() for _ in range(3)]
     prefill_s, token = sorted(runs)[1]
     print(f"[bench] prefill {a.prompt} tokens in {prefill_s * 1e3:.1f} ms (median of 3 after a warm-up pass)",
@@ -470,25 +508,7 @@ def main() -> None:
         print(f"[bench] decode with sampling (T 0.7, top-k 40, top-p 0.9): {sampled:.1f} tok/s", file=sys.stderr,
               flush=True)
 
-    # decode attention alone (one layer's launch pair, HIP events), at the middle and the end
-    # of the timed window; Gemma-3 at a local (sliding) and a global layer. Bytes: the K and V
-    # rows of every attended key (min(pos + 1, window) keys x kv_heads x head_dim x 2).
-    attn = []
-    esz = 2 if a.kv == "f16" else 4
-    cfg = eng.config
-    gemma = cfg.family == "gemma3"
-    layers = [0, cfg.period - 1] if gemma else [0]
-    for layer in [] if a.no_attention_timing else layers:
-        window = cfg.window if gemma and layer % cfg.period != cfg.period - 1 else context
-        for p in sorted({pos + a.steps // 2, pos + a.steps}):
-            if p >= context:
-                continue
-            us = eng.attention_timing(layer, p, 50)
-            nbytes = min(p + 1, window) * spec.kv_heads * spec.head_dim * 2 * esz
-            attn.append({"layer": layer, "pos": p, "keys": min(p + 1, window), "us": us, "bytes": nbytes,
-                         "GBps": nbytes / us / 1e3, "frac": nbytes / us / 1e3 / (PEAK_HBM / 1e9)})
-            print(f"[bench] decode attention layer {layer} at position {p}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s "
-                  f"({100 * nbytes / us / 1e3 / (PEAK_HBM / 1e9):.1f}% of 8 TB/s)", file=sys.stderr, flush=True)
+    attn = [] if a.no_attention_timing else attention_timings(eng, a, spec, context, pos)
 
     result = {
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
