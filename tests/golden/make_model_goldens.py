@@ -26,9 +26,10 @@ A free-running run that settles on one repeated token tests little beyond a fixe
 and a margin screen favours exactly those runs (a repeated token wins by a wide margin).
 So the tied-head shapes use signed output norms (see webgpu_amd/synth.py), and their seeds
 were screened on the device for both the margins (1.3e-3) and diversity: Qwen3-0.6B, at
-least 64 distinct tokens in 256 (2 of seeds 7-399: 314, 397, and 334); Gemma at 1280
-tokens, 24 of 32 (seeds 7, 8, 9 passed); Gemma at 8192 tokens, 36 of 48 (seeds 12, 17,
-25). The fixture records the distinct count.
+least 64 distinct tokens in 256 (4 of seeds 7-399 passed: 62, 314, 334, 397); Gemma at 1280
+tokens, 24 of 32 (10 of seeds 7-39, the first 7, 8, 9); Gemma at 8192 tokens, 36 of 48 (6 of
+seeds 7-39, the first 12, 17, 25). The oracle then confirms them in the order given with
+--seeds (397, 314, 334 / 7, 8, 9 / 12, 17, 25). The fixture records the distinct count.
 
     python tests/golden/make_model_goldens.py [name ...] [--seeds 613,739]
 """
