@@ -440,7 +440,7 @@ static bool attn_plan(const AttnArgs &in, uint64_t partial_floats, AttnPlan &p) 
     const uint32_t nqt = (in.batch + 15) / 16;
     const uint32_t wgs = in.kv_heads * ((nqt * group + 3) / 4);
     tiles = (keys + AP_T - 1) / AP_T;
-    want = ((uint32_t)device_cu_count() + wgs - 1) / wgs;
+    want = ((uint32_t)device_cu_count() * 2 + wgs - 1) / wgs;  // two workgroups per CU: a second wavefront per SIMD
   } else {
     p.qb = group >= 16 ? 1 : 16 / group;
     if (p.qb > in.batch) p.qb = in.batch;
