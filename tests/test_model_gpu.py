@@ -75,9 +75,8 @@ def test_tiny_check_dense_tokens_and_logits():
     # prompt seed 9: the oracle's 4 greedy tokens all differ (the seed-7 prompt repeats one)
     eng, ora, ids, toks = check_model("tiny", 8, 4, seed=9)
     ora.close()
-    eng.dispose()
-    assert len(set(toks)) == 4, toks
     try:
+        assert len(set(toks)) == 4, toks
         # The same tokens through the public token loop (prefill + on-device greedy decode).
         events = list(eng.generate(ids, GenerationOptions(temperature=0, maxTokens=4)))
         assert [e.token for e in events] == toks
@@ -145,7 +144,7 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 def load_fixture(name):
     import xxhash
     z = np.load(os.path.join(GOLDEN, f"model_{name}.npz"), allow_pickle=False)
-    f = synth.build(str(z["model"]))
+    f = synth.build(str(z["model"]) if "model" in z.files else name)  # older fixtures name the model by file
     assert xxhash.xxh64(memoryview(f)).hexdigest() == str(z["gguf_xxh64"]), \
         f"{name}: the synthetic GGUF differs from the one the fixture was made from"
     return f, z
