@@ -556,8 +556,10 @@ __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t 
 #pragma unroll
   for (int e = 0; e < 8; e++) v[e] = glu_act(g[e], act) * u[e];
   const float4 a = make_float4(v[0], v[1], v[2], v[3]), b = make_float4(v[4], v[5], v[6], v[7]);
-  *(float4 *)(y + (uint64_t)tok * R + k) = a;
-  *(float4 *)(y + (uint64_t)tok * R + k + 4) = b;
+  if (y) {
+    *(float4 *)(y + (uint64_t)tok * R + k) = a;
+    *(float4 *)(y + (uint64_t)tok * R + k + 4) = b;
+  }
   split_store8(xs, R, tok, k, a, b);
 }
 
@@ -709,12 +711,13 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
     const uint32_t R = g.job[0].w->rows, count = batch * (R / 8);
     const dim3 grid((count + 255) / 256);
     const float *part = q.part;
+    float *y = g.glu_f32 ? g.glu_out : nullptr;
     if (splits <= 2)
-      hipLaunchKernelGGL(k_glu_reduce<2>, grid, dim3(256), 0, s, part, splits, R, batch, g.glu_out, scratch->xs, g.glu_act);
+      hipLaunchKernelGGL(k_glu_reduce<2>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act);
     else if (splits <= 4)
-      hipLaunchKernelGGL(k_glu_reduce<4>, grid, dim3(256), 0, s, part, splits, R, batch, g.glu_out, scratch->xs, g.glu_act);
+      hipLaunchKernelGGL(k_glu_reduce<4>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act);
     else
-      hipLaunchKernelGGL(k_glu_reduce<MAX_SPLITS>, grid, dim3(256), 0, s, part, splits, R, batch, g.glu_out, scratch->xs,
+      hipLaunchKernelGGL(k_glu_reduce<MAX_SPLITS>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs,
                          g.glu_act);
     WGD_HIP(hipGetLastError());
     scratch->xs_of = g.glu_out; scratch->xs_cols = R; scratch->xs_batch = batch;

@@ -100,6 +100,8 @@ struct GemmGroup {
   GemmJob job[3]; uint32_t n = 0;
   bool accumulate = false;
   float *glu_out = nullptr; int glu_act = 0;
+  // the GLU finish also stores glu_out in f32 (off when only its split is read next)
+  bool glu_f32 = true;
   // leave the split-K partials (one split too) in scratch->p for the caller's own finish;
   // the number of splits is returned in *splits
   bool keep_partials = false; uint32_t *splits = nullptr;

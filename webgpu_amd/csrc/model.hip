@@ -298,8 +298,10 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
     WGD_HIP(ro.first);
     if (!ro.second) WGD_HIP(norm_for(L.ffn_norm, L.up));
     float *ffn_in = m->up;
-    const GemmGroup gu = glu_group(m, L);
+    GemmGroup gu = glu_group(m, L);
     if (c.ffn_gate && gemm_splits_input(L.up, &gs, n) && gemm_group_ok(gu, n)) {
+      // prod in f32 only when the down projection cannot read its split
+      gu.glu_f32 = !gemm_splits_input(L.down, &gs, n);
       WGD_HIP(gemm_group(s, gu, m->normed, n, &gs));  // leaves the split of prod in gs.xs
       ffn_in = m->prod;
     } else if (c.ffn_gate) {
