@@ -606,10 +606,12 @@ bool gemm_group_ok(const GemmGroup &g, uint32_t batch) {
 // at least one 256-column block (64 columns when every matrix is Q8_0), and no more partial
 // sums than the scratch holds.
 static uint32_t group_kspan(const GemmGroup &g, uint32_t batch, uint64_t scratch_floats, uint32_t *rows_total) {
-  uint32_t align = QG_K, tiles = 0, rows = 0;
+  // splits end on K tiles (each chunk reads its own block's header, so a split may start
+  // inside a 256-column super-block): finer splits fill the chip closer to its target
+  const uint32_t align = QG_K;
+  uint32_t tiles = 0, rows = 0;
   for (uint32_t j = 0; j < g.n; j++) {
     const Matrix &w = *g.job[j].w;
-    if (w.type != Q8_0 && w.type != Q4_0) align = 256;
     tiles += (w.rows + QG_M - 1) / QG_M;
     rows += w.rows;
   }
