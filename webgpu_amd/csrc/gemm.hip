@@ -541,7 +541,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(QGemm a, uint32_t splits) {
 // token. S >= splits.
 template <uint32_t S>
 __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t splits, uint32_t R, uint32_t batch,
-                                                    float *y, uint16_t *xs, int act) {
+                                                    float *y, uint16_t *xs, int act, DeferredNorm dn) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i >= batch * (R / 8)) return;
   const uint32_t tok = i / (R / 8), k = (i % (R / 8)) * 8;
@@ -550,8 +550,13 @@ __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t 
   const uint32_t sb = (uint32_t)(4 * n), og = (uint32_t)(4 * (row + k)), ou = og + 4 * R;
   const float4 g0 = split_sum4<S>(rp, splits, sb, og), g1 = split_sum4<S>(rp, splits, sb, og + 16);
   const float4 u0 = split_sum4<S>(rp, splits, sb, ou), u1 = split_sum4<S>(rp, splits, sb, ou + 16);
-  const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-  const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  if (dn.sq) {
+    const float xinv = deferred_inv(dn, tok);
+#pragma unroll
+    for (int e = 0; e < 8; e++) { g[e] *= xinv; u[e] *= xinv; }
+  }
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) v[e] = glu_act(g[e], act) * u[e];
@@ -715,12 +720,14 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
     const float *part = q.part;
     float *y = g.glu_f32 ? g.glu_out : nullptr;
     if (splits <= 2)
-      hipLaunchKernelGGL(k_glu_reduce<2>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act);
+      hipLaunchKernelGGL(k_glu_reduce<2>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act,
+                         g.glu_norm);
     else if (splits <= 4)
-      hipLaunchKernelGGL(k_glu_reduce<4>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act);
+      hipLaunchKernelGGL(k_glu_reduce<4>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act,
+                         g.glu_norm);
     else
       hipLaunchKernelGGL(k_glu_reduce<MAX_SPLITS>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs,
-                         g.glu_act);
+                         g.glu_act, g.glu_norm);
     WGD_HIP(hipGetLastError());
     scratch->xs_of = g.glu_out; scratch->xs_cols = R; scratch->xs_batch = batch;
   } else if (g.keep_partials) {

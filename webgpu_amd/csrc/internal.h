@@ -96,12 +96,26 @@ bool gemm_splits_input(const Matrix &w, const GemmScratch *scratch, uint32_t bat
 // there, [batch][rows], and its split into scratch->xs for the GEMM that reads it; the
 // jobs' own y are not written.
 struct GemmJob { const Matrix *w = nullptr; float *y = nullptr; uint32_t stride = 0, row_base = 0; };
+// An RMSNorm left to the consumer of a GEMM: the GEMM's input was the split of x * w (the
+// norm weight) and the products are scaled per token by 1 / sqrt(sum(x^2) / n + eps), the
+// token's sum of squares being sq[tok * segs + 0 .. segs) added in that order. sq == null:
+// the input was normed already.
+struct DeferredNorm { const float *sq = nullptr; uint32_t segs = 0, n = 0; float eps = 0.f; };
+#ifdef __HIPCC__
+__device__ __forceinline__ float deferred_inv(const DeferredNorm &d, uint32_t tok) {
+  if (!d.sq) return 1.f;
+  float t = 0.f;
+  for (uint32_t u = 0; u < d.segs; u++) t += d.sq[(uint64_t)tok * d.segs + u];
+  return 1.f / sqrtf(t / (float)d.n + d.eps);
+}
+#endif
 struct GemmGroup {
   GemmJob job[3]; uint32_t n = 0;
   bool accumulate = false;
   float *glu_out = nullptr; int glu_act = 0;
   // the GLU finish also stores glu_out in f32 (off when only its split is read next)
   bool glu_f32 = true;
+  DeferredNorm glu_norm;  // the input's pending RMSNorm, applied to gate and up in the GLU finish
   // leave the split-K partials (one split too) in scratch->p for the caller's own finish;
   // the number of splits is returned in *splits
   bool keep_partials = false; uint32_t *splits = nullptr;
@@ -142,6 +156,12 @@ hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_
                 uint32_t batch);
 // Per token: state += the split-K partial sums part[z][tok][n] (in split order), then
 // norm_split() of the new state into y and xs (n % 64 == 0, n <= 16384).
+// The deferred-norm form of reduce_norm_split: state += the partials (split order), xs = the
+// split of state * w, and each token's sum of squares of state in residual_split_segs(n)
+// segments to sq, for a consumer that applies the norm factor (DeferredNorm).
+uint32_t residual_split_segs(uint32_t n);
+hipError_t residual_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, uint16_t *xs,
+                          float *sq, uint32_t n, uint32_t batch);
 hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
                              uint16_t *xs, uint32_t n, float eps, uint32_t batch);
 // norm() that also writes its output in the prompt GEMM's split form into xs (n % 64 == 0).
@@ -162,6 +182,7 @@ struct QKVFinish {
   uint32_t heads = 0, kvh = 0, hd = 0, rot = 0, start = 0; const int32_t *start_dev = nullptr;
   float eps = 0.f; int mode = 1;
   const float2 *cs = nullptr;  // rope_table() of the batch's positions
+  DeferredNorm xnorm;          // the GEMM input's pending RMSNorm, applied to the sums first
 };
 hipError_t qkv_finish(hipStream_t s, const QKVFinish &a);
 // cs[t * rot/2 + i] = (cos, sin) of (start + t) * scale * theta^(-2i/rot) for t < n (angles in

@@ -67,6 +67,7 @@ struct wgd_model {
   int32_t *argmax_buf = nullptr;
   uint64_t *arg_part = nullptr; uint32_t arg_entries = 0;  // head argmax keys (quantized path)
   float *att_part = nullptr; uint64_t att_part_floats = 0;
+  float *res_sq = nullptr;        // per-token segment sums of squares of a deferred prompt RMSNorm
   GemmScratch gemm_part;          // split-K partial sums of the prompt GEMMs
   // Quantized-activation decode path (every matrix Q4_K, Q6_K or Q8_0): activation buffers
   // in the QX format.
@@ -235,18 +236,30 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       WGD_HIP(rope_table(s, m->rope_batch[1], c.head_dim, n, start, start_dev, r1.theta, r1.scale));
     }
   }
+  // The input norm of the next GEMM group is deferred into that group's finish (DeferredNorm)
+  // while dn.sq is set: the split in gs.xs then holds x * w, not the normed x.
+  DeferredNorm dn;
   // A residual projection (O, down) into m->hidden: with the next RMSNorm fused into its
-  // split-K finish when that norm feeds a split-input GEMM (then returns true: m->normed and
-  // its split are ready), else added by the GEMM's own reduction, else the generic path.
+  // split-K finish when that norm feeds a split-input GEMM (then returns true: the split of
+  // m->normed is ready), else added by the GEMM's own reduction, else the generic path. When
+  // the GEMM group after the norm has its own finish (`deferred`: the grouped Q/K/V or
+  // gate/up), the norm factor is left to that finish, so the residual finish needs no
+  // row-wide sum and spreads over every CU; otherwise one workgroup per token forms the norm
+  // and writes m->normed as well.
   auto residual = [&](const Matrix &W, const float *x, const float *bias_w, const float *post_w,
-                      const float *next_w, const Matrix *next_first) -> std::pair<hipError_t, bool> {
+                      const float *next_w, const Matrix *next_first, bool deferred) -> std::pair<hipError_t, bool> {
     if (!gemma && !bias_w && gemm_splits_input(W, &gs, n)) {
-      if (next_w && next_first && gemm_splits_input(*next_first, &gs, n) && H <= 16384) {
+      if (next_w && next_first && gemm_splits_input(*next_first, &gs, n) && (deferred || H <= 16384)) {
         GemmGroup g = res_group(m, W);
         uint32_t splits = 0;
         g.splits = &splits;
         hipError_t e = gemm_group(s, g, x, n, &gs);
-        if (e == hipSuccess) e = reduce_norm_split(s, gs.p, splits, m->hidden, next_w, m->normed, gs.xs, H, c.epsilon, n);
+        if (e == hipSuccess && deferred) {
+          e = residual_split(s, gs.p, splits, m->hidden, next_w, gs.xs, m->res_sq, H, n);
+          dn = DeferredNorm{m->res_sq, residual_split_segs(H), H, c.epsilon};
+        } else if (e == hipSuccess) {
+          e = reduce_norm_split(s, gs.p, splits, m->hidden, next_w, m->normed, gs.xs, H, c.epsilon, n);
+        }
         gs.xs_of = m->normed; gs.xs_cols = H; gs.xs_batch = n;
         return {e, true};
       }
@@ -257,15 +270,25 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
     if (e == hipSuccess) e = gemma ? norm_add(s, m->proj, post_w, m->hidden, H, c.epsilon, n) : add(s, m->proj, m->hidden, n * H);
     return {e, false};
   };
-  bool normed_ready = false;  // m->normed (and its split) already hold this layer's attention-norm input
+  // whether a layer's Q/K/V, and its gate/up, run as one grouped GEMM with its own finish
+  auto qkv_fused = [&](const Layer &L) {
+    return m->rope_batch[0] && gemm_splits_input(L.q, &gs, n) && gemm_group_ok(qkv_group(m, L), n);
+  };
+  auto glu_fused = [&](const Layer &L) {
+    return c.ffn_gate && gemm_splits_input(L.up, &gs, n) && gemm_group_ok(glu_group(m, L), n);
+  };
+  bool normed_ready = false;  // the split of this layer's attention-norm input is ready (dn: deferred)
   for (int l = 0; l < c.layers; l++) {
     Layer &L = m->L[l];
-    if (!normed_ready) WGD_HIP(norm_for(L.attn_norm, L.q));
+    if (!normed_ready) {
+      WGD_HIP(norm_for(L.attn_norm, L.q));
+      dn = DeferredNorm{};
+    }
     normed_ready = false;
     GemmGroup qkv = qkv_group(m, L);
     uint32_t splits = 0;
     qkv.keep_partials = true; qkv.splits = &splits;
-    if (m->rope_batch[0] && gemm_splits_input(L.q, &gs, n) && gemm_group_ok(qkv, n)) {
+    if (qkv_fused(L)) {
       // Q/K/V partial sums finished in one pass: bias, RoPE, K/V into the ring
       WGD_HIP(gemm_group(s, qkv, m->normed, n, &gs));
       const RopeParams r = rope_params(m, l);
@@ -278,7 +301,9 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       f.start = start; f.start_dev = start_dev;
       f.eps = r.eps; f.mode = r.mode;
       f.cs = m->rope_batch[gemma && local_layer(m, l) ? 1 : 0];
+      f.xnorm = dn;
       WGD_HIP(qkv_finish(s, f));
+      dn = DeferredNorm{};
       // the attention output's split for the O GEMM comes from the key-split merge
       bool written = false;
       const bool want = gemm_splits_input(L.o, &gs, n);
@@ -294,14 +319,19 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
       WGD_HIP(attention_block(m, l, n, start, start_dev));
       gs.xs_of = nullptr;
     }
-    auto ro = residual(L.o, m->att, L.bo, L.post_attn, L.ffn_norm, &L.up);
+    auto ro = residual(L.o, m->att, L.bo, L.post_attn, L.ffn_norm, &L.up, glu_fused(L));
     WGD_HIP(ro.first);
-    if (!ro.second) WGD_HIP(norm_for(L.ffn_norm, L.up));
+    if (!ro.second) {
+      WGD_HIP(norm_for(L.ffn_norm, L.up));
+      dn = DeferredNorm{};
+    }
     float *ffn_in = m->up;
     GemmGroup gu = glu_group(m, L);
-    if (c.ffn_gate && gemm_splits_input(L.up, &gs, n) && gemm_group_ok(gu, n)) {
+    if (glu_fused(L)) {
       // prod in f32 only when the down projection cannot read its split
       gu.glu_f32 = !gemm_splits_input(L.down, &gs, n);
+      gu.glu_norm = dn;
+      dn = DeferredNorm{};
       WGD_HIP(gemm_group(s, gu, m->normed, n, &gs));  // leaves the split of prod in gs.xs
       ffn_in = m->prod;
     } else if (c.ffn_gate) {
@@ -322,7 +352,7 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
     }
     const bool last = l + 1 == c.layers;
     auto rd = residual(L.down, ffn_in, nullptr, L.post_ffw, last ? nullptr : m->L[l + 1].attn_norm,
-                       last ? nullptr : &m->L[l + 1].q);
+                       last ? nullptr : &m->L[l + 1].q, !last && qkv_fused(m->L[l + 1]));
     WGD_HIP(rd.first);
     normed_ready = rd.second;
   }
@@ -640,6 +670,7 @@ int wgd_model_create(wgd_context *ctx, const wgd_model_config *cfg, const int32_
   rc = rc ? rc : alloc_t(m, B * F, "up", &m->up);
   rc = rc ? rc : alloc_t(m, B * F, "product", &m->prod);
   rc = rc ? rc : alloc_t(m, B * H, "down", &m->down);
+  rc = rc ? rc : alloc_t(m, B * residual_split_segs((uint32_t)H), "deferred norm sums", &m->res_sq);
   rc = rc ? rc : alloc_t(m, (uint64_t)c.vocab, "logits", &m->logits);
   rc = rc ? rc : alloc_t(m, B, "ids", &m->ids);
   rc = rc ? rc : alloc_t(m, 1, "step state", &m->state);

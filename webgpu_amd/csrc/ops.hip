@@ -121,6 +121,53 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
   }
 }
 
+// The deferred-norm finish of a residual projection: one 128-thread workgroup per token and
+// segment of RS_E elements (eight per thread), so the partials stream over every CU. The
+// segment's sum of squares: each thread's eight in order, the DPP fold of each wavefront,
+// then the two wavefronts in order.
+constexpr uint32_t RS_T = 128, RS_E = 8 * RS_T;
+uint32_t residual_split_segs(uint32_t n) { return (n + RS_E - 1) / RS_E; }
+__global__ __launch_bounds__(128) void k_residual_split(const float *part, uint32_t splits, float *state,
+                                                        const float *w, uint16_t *xs, float *sq, uint32_t n,
+                                                        uint32_t batch) {
+  __shared__ float red[RS_T / 64];
+  const uint32_t seg = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t stride = (uint64_t)n * batch;
+  const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, splits, stride);
+  const uint32_t k = seg * RS_E + 8 * tid;
+  float ss = 0.f;
+  if (k < n) {
+    float *sr = state + (uint64_t)tok * n + k;
+    const uint32_t off = 4 * (tok * n + k);
+    float4 a = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off);
+    float4 b = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off + 16);
+    const float4 ha = *(const float4 *)sr, hb = *(const float4 *)(sr + 4);
+    a = make_float4(ha.x + a.x, ha.y + a.y, ha.z + a.z, ha.w + a.w);
+    b = make_float4(hb.x + b.x, hb.y + b.y, hb.z + b.z, hb.w + b.w);
+    *(float4 *)sr = a;
+    *(float4 *)(sr + 4) = b;
+    ss = a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+    const float4 wa = *(const float4 *)(w + k), wb = *(const float4 *)(w + k + 4);
+    split_store8(xs, n, tok, k, make_float4(a.x * wa.x, a.y * wa.y, a.z * wa.z, a.w * wa.w),
+                 make_float4(b.x * wb.x, b.y * wb.y, b.z * wb.z, b.w * wb.w));
+  }
+  ss = wave_total(ss);
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  if (tid == 0) sq[(uint64_t)tok * gridDim.x + seg] = red[0] + red[1];
+}
+
+hipError_t residual_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, uint16_t *xs,
+                          float *sq, uint32_t n, uint32_t batch) {
+  if (!batch) return hipSuccess;
+  if (n % SPLIT_K || !splits || splits > MAX_SPLITS || (uint64_t)splits * n * batch * 4 >= (1ull << 31) || !sq ||
+      ((uintptr_t)part | (uintptr_t)state | (uintptr_t)w) % 16)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_residual_split, dim3(residual_split_segs(n), batch), dim3(RS_T), 0, s, part, splits, state, w,
+                     xs, sq, n, batch);
+  return hipGetLastError();
+}
+
 hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
                              uint16_t *xs, uint32_t n, float eps, uint32_t batch) {
   if (!batch) return hipSuccess;
@@ -333,8 +380,10 @@ __global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
   const uint64_t n = (uint64_t)a.rows_total * a.batch, base = (uint64_t)tok * a.rows_total + (uint64_t)slot * hd;
   float *v = buf[wv];
   const __amdgpu_buffer_rsrc_t rp = split_rsrc(a.part, a.splits, n);
+  const float xinv = deferred_inv(a.xnorm, tok);
   for (uint32_t d = lane; d < hd; d += 64) {
-    const float acc = split_sum<MAX_SPLITS>(rp, a.splits, (uint32_t)(4 * n), (uint32_t)(4 * (base + d)));
+    float acc = split_sum<MAX_SPLITS>(rp, a.splits, (uint32_t)(4 * n), (uint32_t)(4 * (base + d)));
+    if (a.xnorm.sq) acc *= xinv;
     v[d] = bias ? acc + bias[h * hd + d] : acc;
   }
   __builtin_amdgcn_wave_barrier();
