@@ -119,9 +119,9 @@ int wgd_matvec(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_bu
                uint32_t cols, uint32_t rows, uint32_t row_base);
 /* wgd_matvec once per launch shape that the decode step's launch-shape measurement may pick
  * for this matrix and input (the cost-model shape first; F16/F32 matrices have none): shape k
- * writes y[k * rows + r], for k < *count <= max_shapes. Every shape computes the same bits,
- * which is what a caller checks with it; no reference counterpart (the measurement is this
- * library's own). */
+ * writes y[k * rows + r], for k < *count <= max_shapes, and y must hold max_shapes * rows
+ * floats. Every shape computes the same bits, which is what a caller checks with it; no
+ * reference counterpart (the measurement is this library's own). */
 int wgd_matvec_shapes(wgd_context *ctx, int32_t type, const wgd_buffer *w, const wgd_buffer *qx, wgd_buffer *y,
                       uint32_t cols, uint32_t rows, uint32_t max_shapes, uint32_t *count);
 /* decodeWeight (src/core/quant.ts:6-29) for `count` consecutive elements: out[i] =
