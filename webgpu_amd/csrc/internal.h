@@ -154,14 +154,14 @@ hipError_t embed(hipStream_t s, int type, const uint8_t *table, const int32_t *i
                  uint32_t hidden, uint32_t n, double scale);
 hipError_t norm(hipStream_t s, const float *x, const float *w, float *y, uint32_t n, float eps,
                 uint32_t batch);
-// Per token: state += the split-K partial sums part[z][tok][n] (in split order), then
-// norm_split() of the new state into y and xs (n % 64 == 0, n <= 16384).
 // The deferred-norm form of reduce_norm_split: state += the partials (split order), xs = the
 // split of state * w, and each token's sum of squares of state in residual_split_segs(n)
 // segments to sq, for a consumer that applies the norm factor (DeferredNorm).
 uint32_t residual_split_segs(uint32_t n);
 hipError_t residual_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, uint16_t *xs,
                           float *sq, uint32_t n, uint32_t batch);
+// Per token: state += the split-K partial sums part[z][tok][n] (in split order), then
+// norm_split() of the new state into y and xs (n % 64 == 0, n <= 16384).
 hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
                              uint16_t *xs, uint32_t n, float eps, uint32_t batch);
 // norm() that also writes its output in the prompt GEMM's split form into xs (n % 64 == 0).
