@@ -929,11 +929,18 @@ __global__ __launch_bounds__(256) void k_attn_dec2(AttnDecK a) {
 // first AD_ZB chunks' outputs in registers; chunks at or past the active count are masked
 // afterwards. So the merge is one round trip.
 constexpr uint32_t AD_MAX_SPLITS = 1024, AD_ZB = 32;
+//
+// With group > 0 (kv heads a multiple of 8) workgroup w, dispatched to XCD w % 8, merges a
+// head of a kv head kv with kv % 8 == w % 8: the chunk launch's workgroup z * kv_heads + kv
+// ran on that XCD, so the head's partials were written through its L2.
 __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, QXOut qx, const int32_t *pos_dev,
-                                                   uint32_t window, uint32_t chunk, uint32_t nsplit, uint32_t hd) {
+                                                   uint32_t window, uint32_t chunk, uint32_t nsplit, uint32_t hd,
+                                                   uint32_t group) {
   __shared__ float wz[AD_MAX_SPLITS];
   __shared__ float red[8];
-  const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wv = d >> 6, nw = (blockDim.x + 63) >> 6;
+  const uint32_t w = blockIdx.x, j = w / 8;
+  const uint32_t h = group ? (w % 8 + 8 * (j / group)) * group + j % group : w;
+  const uint32_t d = threadIdx.x, lane = d & 63, wv = d >> 6, nw = (blockDim.x + 63) >> 6;
   const uint32_t stride = hd + 2;
   const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(part + (uint64_t)h * nsplit * stride), 0, (int)(nsplit * stride * 4), 0x00020000);
@@ -1072,8 +1079,9 @@ hipError_t decode_attention(hipStream_t s, const DecodeAttnArgs &in) {
   else launch_dec<4>(s, k, grid, in.kv16);
   WGD_HIP(hipGetLastError());
   const uint32_t threads = (in.hd + 63) / 64 * 64;
+  const uint32_t group = in.kv_heads % 8 == 0 ? k.group : 0;
   hipLaunchKernelGGL(k_attn_comb, dim3(in.heads), dim3(threads), 0, s, (const float *)in.partial, in.y, in.qx,
-                     in.pos, in.window, k.chunk, k.nsplit, in.hd);
+                     in.pos, in.window, k.chunk, k.nsplit, in.hd, group);
   return hipGetLastError();
 }
 
