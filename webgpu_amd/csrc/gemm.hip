@@ -536,15 +536,10 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(QGemm a, uint32_t splits) {
   }
 }
 
-// gate (rows [0, R)) and up (rows [R, 2R)) from the split-K partials, then act(gate) * up
-// into y [batch][R] and its split form for the down GEMM: one thread per eight columns of a
-// token. S >= splits.
+// The GLU finish (k_glu_reduce) of columns k .. k + 7 of token tok.
 template <uint32_t S>
-__global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t splits, uint32_t R, uint32_t batch,
-                                                    float *y, uint16_t *xs, int act, DeferredNorm dn) {
-  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= batch * (R / 8)) return;
-  const uint32_t tok = i / (R / 8), k = (i % (R / 8)) * 8;
+__device__ __forceinline__ void glu_finish8(const float *part, uint32_t splits, uint32_t R, uint32_t batch, float *y,
+                                            uint16_t *xs, int act, const DeferredNorm &dn, uint32_t tok, uint32_t k) {
   const uint64_t n = (uint64_t)2 * R * batch, row = (uint64_t)tok * 2 * R;
   const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, splits, n);
   const uint32_t sb = (uint32_t)(4 * n), og = (uint32_t)(4 * (row + k)), ou = og + 4 * R;
@@ -566,6 +561,28 @@ __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t 
     *(float4 *)(y + (uint64_t)tok * R + k + 4) = b;
   }
   split_store8(xs, R, tok, k, a, b);
+}
+
+// gate (rows [0, R)) and up (rows [R, 2R)) from the split-K partials, then act(gate) * up
+// into y [batch][R] and its split form for the down GEMM: one thread per eight columns of a
+// token. S >= splits.
+//
+// The GEMM's 128-row tile t ran on XCD t % 8 (its grid's first dimension, the tile count, is
+// a multiple of 8, and workgroups go to the XCDs round-robin), and with R a multiple of 1024
+// the up tile of a column has the gate tile's residue. Then (by_xcd) workgroup w, on XCD
+// w % 8, takes token w / 8 and the columns of the tiles t = w (mod 8), reading partials
+// written through its own L2; otherwise workgroup w takes 256 consecutive column groups.
+template <uint32_t S>
+__global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t splits, uint32_t R, uint32_t batch,
+                                                    float *y, uint16_t *xs, int act, DeferredNorm dn, uint32_t by_xcd) {
+  if (!by_xcd) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < batch * (R / 8)) glu_finish8<S>(part, splits, R, batch, y, xs, act, dn, i / (R / 8), (i % (R / 8)) * 8);
+    return;
+  }
+  const uint32_t x = blockIdx.x % 8, tok = blockIdx.x / 8;
+  for (uint32_t j = threadIdx.x; j < R / 64; j += 256)
+    glu_finish8<S>(part, splits, R, batch, y, xs, act, dn, tok, (x + 8 * (j / 16)) * 128 + (j % 16) * 8);
 }
 
 static bool qgemm_supported(const Matrix &w) {
@@ -716,18 +733,19 @@ hipError_t gemm_group(hipStream_t s, const GemmGroup &g, const float *x, uint32_
   WGD_HIP(hipGetLastError());
   if (g.glu_out) {
     const uint32_t R = g.job[0].w->rows, count = batch * (R / 8);
-    const dim3 grid((count + 255) / 256);
+    const uint32_t by_xcd = R % 1024 == 0 && tiles % 8 == 0 ? 1u : 0u;
+    const dim3 grid(by_xcd ? batch * 8 : (count + 255) / 256);
     const float *part = q.part;
     float *y = g.glu_f32 ? g.glu_out : nullptr;
     if (splits <= 2)
       hipLaunchKernelGGL(k_glu_reduce<2>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act,
-                         g.glu_norm);
+                         g.glu_norm, by_xcd);
     else if (splits <= 4)
       hipLaunchKernelGGL(k_glu_reduce<4>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs, g.glu_act,
-                         g.glu_norm);
+                         g.glu_norm, by_xcd);
     else
       hipLaunchKernelGGL(k_glu_reduce<MAX_SPLITS>, grid, dim3(256), 0, s, part, splits, R, batch, y, scratch->xs,
-                         g.glu_act, g.glu_norm);
+                         g.glu_act, g.glu_norm, by_xcd);
     WGD_HIP(hipGetLastError());
     scratch->xs_of = g.glu_out; scratch->xs_cols = R; scratch->xs_batch = batch;
   } else if (g.keep_partials) {

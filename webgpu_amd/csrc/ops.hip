@@ -122,21 +122,32 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
 }
 
 // The deferred-norm finish of a residual projection: one 128-thread workgroup per token and
-// segment of RS_E elements (eight per thread), so the partials stream over every CU. The
-// segment's sum of squares: each thread's eight in order, the DPP fold of each wavefront,
-// then the two wavefronts in order.
+// segment, eight elements per thread a step, so the partials stream over every CU; each
+// segment's sum of squares goes to sq (each thread's elements in order, the DPP fold of
+// each wavefront, then the two wavefronts in order).
+//
+// The segments follow the split-K GEMM that wrote the partials. Its 128-row tile t ran on
+// XCD t % 8 (its grid's first dimension is the tile count, a multiple of 8 here, and
+// workgroups are dispatched to the XCDs round-robin). So when n is a multiple of 1024,
+// segment x holds the tiles t = x (mod 8), and workgroup (x, token), dispatched to XCD x,
+// reads partials written through its own L2. Otherwise segment x is elements
+// [RS_E x, RS_E (x + 1)).
 constexpr uint32_t RS_T = 128, RS_E = 8 * RS_T;
-uint32_t residual_split_segs(uint32_t n) { return (n + RS_E - 1) / RS_E; }
+static bool residual_by_xcd(uint32_t n) { return n % 1024 == 0; }
+uint32_t residual_split_segs(uint32_t n) { return residual_by_xcd(n) ? 8 : (n + RS_E - 1) / RS_E; }
 __global__ __launch_bounds__(128) void k_residual_split(const float *part, uint32_t splits, float *state,
                                                         const float *w, uint16_t *xs, float *sq, uint32_t n,
-                                                        uint32_t batch) {
+                                                        uint32_t batch, uint32_t by_xcd) {
   __shared__ float red[RS_T / 64];
   const uint32_t seg = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint64_t stride = (uint64_t)n * batch;
   const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, splits, stride);
-  const uint32_t k = seg * RS_E + 8 * tid;
+  // this thread's groups of eight: group j of the segment starts at element col(j)
+  const uint32_t groups = by_xcd ? n / 64 : (seg * RS_E + RS_E <= n ? RS_E : n - seg * RS_E) / 8;
+  auto col = [&](uint32_t j) { return by_xcd ? (seg + 8 * (j / 16)) * 128 + (j % 16) * 8 : seg * RS_E + 8 * j; };
   float ss = 0.f;
-  if (k < n) {
+  for (uint32_t j = tid; j < groups; j += RS_T) {
+    const uint32_t k = col(j);
     float *sr = state + (uint64_t)tok * n + k;
     const uint32_t off = 4 * (tok * n + k);
     float4 a = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off);
@@ -146,7 +157,7 @@ __global__ __launch_bounds__(128) void k_residual_split(const float *part, uint3
     b = make_float4(hb.x + b.x, hb.y + b.y, hb.z + b.z, hb.w + b.w);
     *(float4 *)sr = a;
     *(float4 *)(sr + 4) = b;
-    ss = a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+    ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
     const float4 wa = *(const float4 *)(w + k), wb = *(const float4 *)(w + k + 4);
     split_store8(xs, n, tok, k, make_float4(a.x * wa.x, a.y * wa.y, a.z * wa.z, a.w * wa.w),
                  make_float4(b.x * wb.x, b.y * wb.y, b.z * wb.z, b.w * wb.w));
@@ -164,7 +175,7 @@ hipError_t residual_split(hipStream_t s, const float *part, uint32_t splits, flo
       ((uintptr_t)part | (uintptr_t)state | (uintptr_t)w) % 16)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_residual_split, dim3(residual_split_segs(n), batch), dim3(RS_T), 0, s, part, splits, state, w,
-                     xs, sq, n, batch);
+                     xs, sq, n, batch, residual_by_xcd(n) ? 1u : 0u);
   return hipGetLastError();
 }
 
@@ -367,13 +378,26 @@ hipError_t rope_table(hipStream_t s, float2 *cs, uint32_t rot, uint32_t n, uint3
 // (rotations from rope_table, the same f64 angles) to Q and K heads, and writes Q to q and K / V straight into the
 // ring slot of the token's position (k_kv_append's slot). The head is staged in LDS so any
 // rotary width and pair layout can be read back.
-__global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a) {
+//
+// With hd 128 and a multiple of 8 head slots (by_xcd), slot s is the GEMM's 128-row tile s,
+// which ran on XCD s % 8 (the tile count leads its grid; workgroups go to the XCDs
+// round-robin). Workgroup w, on XCD w % 8, then takes slots s = w (mod 8), so it reads
+// partials written through its own L2; otherwise workgroup w takes items 4w .. 4w + 3.
+__global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a, uint32_t by_xcd) {
   __shared__ float buf[4][512];
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint32_t per = a.heads + 2 * a.kvh, hd = a.hd;
-  const uint32_t item = blockIdx.x * 4 + wv;
-  if (item >= a.batch * per) return;
-  const uint32_t tok = item / per, slot = item % per;
+  uint32_t tok, slot;
+  if (by_xcd) {
+    const uint32_t i = blockIdx.x / 8 * 4 + wv, per8 = per / 8;
+    tok = i / per8;
+    slot = blockIdx.x % 8 + 8 * (i % per8);
+  } else {
+    const uint32_t item = blockIdx.x * 4 + wv;
+    tok = item / per;
+    slot = item % per;
+  }
+  if (tok >= a.batch) return;
   const int kind = slot < a.heads ? 0 : slot < a.heads + a.kvh ? 1 : 2;
   const uint32_t h = kind == 0 ? slot : kind == 1 ? slot - a.heads : slot - a.heads - a.kvh;
   const float *bias = kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv;
@@ -423,8 +447,10 @@ hipError_t qkv_finish(hipStream_t s, const QKVFinish &a) {
   if (a.hd > 512 || a.rot > a.hd || a.rot % 2 || !a.capacity || !a.cs || (a.mode == 0 && (!a.qn || !a.kn)) ||
       !a.splits || a.splits > MAX_SPLITS || (uint64_t)a.splits * a.rows_total * a.batch * 4 >= (1ull << 31))
     return hipErrorInvalidValue;
-  const uint32_t items = a.batch * (a.heads + 2 * a.kvh);
-  hipLaunchKernelGGL(k_qkv_finish, dim3((items + 3) / 4), dim3(256), 0, s, a);
+  const uint32_t per = a.heads + 2 * a.kvh, items = a.batch * per;
+  const uint32_t by_xcd = a.hd == 128 && per % 8 == 0 ? 1u : 0u;
+  const uint32_t groups = by_xcd ? 8 * ((a.batch * (per / 8) + 3) / 4) : (items + 3) / 4;
+  hipLaunchKernelGGL(k_qkv_finish, dim3(groups), dim3(256), 0, s, a, by_xcd);
   return hipGetLastError();
 }
 
