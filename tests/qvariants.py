@@ -15,6 +15,10 @@ the three shaped decoders do not use.
 * ``llama-q80-w96``: every matrix Q8_0 at hidden width 96, which is not a whole 64-column
   tile: the matrices reading the hidden state keep the GGUF layout, so decode runs the
   generic step (batched kernels at one token, the position read from device state).
+* ``llama-xcd``: Q4_K with a Q6_K V at hidden 1024, 16 query x 128 and 8 KV heads, FFN 2048:
+  the widths at which the prompt finishes (Q/K/V, GLU, residual) and the decode attention
+  merge take their work by the XCD that wrote the partials (head dim 128, a multiple of 8
+  head slots and of 8 KV heads, hidden and FFN multiples of 1024).
 
 Dimensions (but for ``llama-q80-w96``) are the smallest the planar K-quant kernels take: hidden 256 (Q4_K/Q6_K rows of
 whole 256-element blocks), 4 query heads x 64, 2 KV heads, FFN 512, vocab 300. Matrix blocks
@@ -28,7 +32,7 @@ from webgpu_amd import synth
 from webgpu_amd.gguf import F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANTS, model_config, parse_gguf_header
 from webgpu_amd.tokenizer import byte_alphabet
 
-KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16", "llama-q80-w96")
+KINDS = ("qwen2-bias", "llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16", "llama-q80-w96", "llama-xcd")
 
 
 CHAT_SPECIALS = ["<|im_start|>", "<|im_end|>", "<|endoftext|>"]
@@ -53,11 +57,13 @@ def build(kind: str, tokenizer: bool = False):
     file also carries a byte-level BPE vocabulary with a ChatML template."""
     rng = np.random.default_rng(sum(kind.encode()) * 31 + 5)
     H, nh, nkv, hd, F, V, L = 256, 4, 2, 64, 512, 300, 2
+    if kind == "llama-xcd":
+        H, nh, nkv, hd, F = 1024, 16, 8, 128, 2048
     w96 = kind == "llama-q80-w96"
     if w96:
         H = 96
     arch = {"qwen2-bias": "qwen2", "llama-partial": "llama", "qwen3-mixed": "qwen3", "llama-q5q4": "llama",
-            "qwen3-f16": "qwen3", "llama-q80-w96": "llama"}[kind]
+            "qwen3-f16": "qwen3", "llama-q80-w96": "llama", "llama-xcd": "llama"}[kind]
     qd, kd = nh * hd, nkv * hd
     T: List[Tuple[str, List[int], int, np.ndarray]] = []
 
@@ -110,7 +116,7 @@ def build(kind: str, tokenizer: bool = False):
     elif kind == "llama-partial":
         meta += [(f"{arch}.rope.freq_base", 6, 1e4), (f"{arch}.rope.dimension_count", 4, 32),
                  (f"{arch}.attention.sliding_window", 4, 24)]
-    elif kind in ("llama-q5q4", "llama-q80-w96"):
+    elif kind in ("llama-q5q4", "llama-q80-w96", "llama-xcd"):
         meta += [(f"{arch}.rope.freq_base", 6, 5e5), (f"{arch}.rope.dimension_count", 4, hd)]
     else:
         meta += [(f"{arch}.rope.freq_base", 6, 1e6), (f"{arch}.rope.dimension_count", 4, 48),

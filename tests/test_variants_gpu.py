@@ -79,7 +79,7 @@ def test_quantized_variant_prefill_and_decode(kind):
         eng.dispose()
 
 
-@pytest.mark.parametrize("kind", ["llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16", "llama-q80-w96"])
+@pytest.mark.parametrize("kind", ["llama-partial", "qwen3-mixed", "llama-q5q4", "qwen3-f16", "llama-q80-w96", "llama-xcd"])
 def test_quantized_variant_graph_decode_matches_eager(kind):
     # the captured per-token graph (quantized matvecs, fused decode attention) against one
     # eager forward per token from the same prefix
