@@ -161,9 +161,10 @@ uint32_t residual_split_segs(uint32_t n);
 hipError_t residual_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, uint16_t *xs,
                           float *sq, uint32_t n, uint32_t batch);
 // Per token: state += the split-K partial sums part[z][tok][n] (in split order), then
-// norm_split() of the new state into y and xs (n % 64 == 0, n <= 16384).
+// norm_split() of the new state into y and xs (n % 64 == 0, n <= 16384). With post_w the
+// sums are a delta added as RMSNorm(delta) * post_w (Gemma's post-norms).
 hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
-                             uint16_t *xs, uint32_t n, float eps, uint32_t batch);
+                             uint16_t *xs, uint32_t n, float eps, uint32_t batch, const float *post_w = nullptr);
 // norm() that also writes its output in the prompt GEMM's split form into xs (n % 64 == 0).
 hipError_t norm_split(hipStream_t s, const float *x, const float *w, float *y, uint16_t *xs, uint32_t n, float eps,
                       uint32_t batch);

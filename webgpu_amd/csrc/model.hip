@@ -248,22 +248,24 @@ hipError_t layers_batched(wgd_model *m, uint32_t n, uint32_t start, const int32_
   // and writes m->normed as well.
   auto residual = [&](const Matrix &W, const float *x, const float *bias_w, const float *post_w,
                       const float *next_w, const Matrix *next_first, bool deferred) -> std::pair<hipError_t, bool> {
-    if (!gemma && !bias_w && gemm_splits_input(W, &gs, n)) {
-      if (next_w && next_first && gemm_splits_input(*next_first, &gs, n) && (deferred || H <= 16384)) {
+    if (!bias_w && gemm_splits_input(W, &gs, n)) {
+      // Gemma's post-norm needs the whole row, so its finish is the per-token one
+      if (next_w && next_first && gemm_splits_input(*next_first, &gs, n) && (gemma ? H <= 16384 : deferred || H <= 16384)) {
         GemmGroup g = res_group(m, W);
         uint32_t splits = 0;
         g.splits = &splits;
         hipError_t e = gemm_group(s, g, x, n, &gs);
-        if (e == hipSuccess && deferred) {
+        if (e == hipSuccess && deferred && !gemma) {
           e = residual_split(s, gs.p, splits, m->hidden, next_w, gs.xs, m->res_sq, H, n);
           dn = DeferredNorm{m->res_sq, residual_split_segs(H), H, c.epsilon};
         } else if (e == hipSuccess) {
-          e = reduce_norm_split(s, gs.p, splits, m->hidden, next_w, m->normed, gs.xs, H, c.epsilon, n);
+          e = reduce_norm_split(s, gs.p, splits, m->hidden, next_w, m->normed, gs.xs, H, c.epsilon, n,
+                                gemma ? post_w : nullptr);
         }
         gs.xs_of = m->normed; gs.xs_cols = H; gs.xs_batch = n;
         return {e, true};
       }
-      return {matmul(s, W, x, m->hidden, H, 0, 0, n, &gs, true), false};
+      if (!gemma) return {matmul(s, W, x, m->hidden, H, 0, 0, n, &gs, true), false};
     }
     hipError_t e = matmul(s, W, x, m->proj, H, 0, 0, n, &gs);
     if (e == hipSuccess) e = bias(s, m->proj, bias_w, n, H);

@@ -70,14 +70,27 @@ __global__ __launch_bounds__(256) void k_norm_split(const float *x, const float 
 
 // The finish of a residual projection (O or down) kept as split-K partials, fused with the
 // RMSNorm that reads the residual next: per token, state += the partials summed in split
-// order, then y = RMSNorm(state) * w and its split form xs. One 512-thread workgroup per
-// token, eight consecutive elements per thread step (n <= RN_G * 8 * 512).
+// order, then y = RMSNorm(state) * w and its split form xs. With post_w (Gemma's post-norms)
+// the summed partials are a delta that enters as RMSNorm(delta) * post_w. One 512-thread
+// workgroup per token, eight consecutive elements per thread step (n <= RN_G * 8 * 512).
 constexpr uint32_t RN_T = 512, RN_G = 4;
+// The sum over the workgroup of each thread's ss, in a fixed order.
+__device__ __forceinline__ float block_total(float ss, float *red) {
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  ss = wave_sum(ss);
+  __syncthreads();  // red is free again
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (uint32_t u = 0; u < RN_T / 64; u++) ss += red[u];
+  return ss;
+}
 __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, uint32_t splits, float *state,
-                                                           const float *w, float *y, uint16_t *xs, uint32_t n,
-                                                           uint32_t batch, float eps) {
+                                                           const float *post_w, const float *w, float *y,
+                                                           uint16_t *xs, uint32_t n, uint32_t batch, float eps) {
   __shared__ float red[RN_T / 64];
-  const uint32_t tok = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t tok = blockIdx.x, tid = threadIdx.x;
   const uint64_t stride = (uint64_t)n * batch;
   const __amdgpu_buffer_rsrc_t rp = split_rsrc(part, splits, stride);
   float *sr = state + (uint64_t)tok * n;
@@ -88,25 +101,37 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
     const uint32_t k = 8 * (tid + RN_T * gi);
     if (k >= n) break;  // uniform per thread
     const uint32_t off = 4 * (tok * n + k);
-    float4 a = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off);
-    float4 b = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off + 16);
-    const float4 ha = *(const float4 *)(sr + k), hb = *(const float4 *)(sr + k + 4);
-    a = make_float4(ha.x + a.x, ha.y + a.y, ha.z + a.z, ha.w + a.w);
-    b = make_float4(hb.x + b.x, hb.y + b.y, hb.z + b.z, hb.w + b.w);
-    *(float4 *)(sr + k) = a;
-    *(float4 *)(sr + k + 4) = b;
+    const float4 a = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off);
+    const float4 b = split_sum4<MAX_SPLITS>(rp, splits, (uint32_t)(4 * stride), off + 16);
     v[gi][0] = a.x; v[gi][1] = a.y; v[gi][2] = a.z; v[gi][3] = a.w;
     v[gi][4] = b.x; v[gi][5] = b.y; v[gi][6] = b.z; v[gi][7] = b.w;
 #pragma unroll
     for (int e = 0; e < 8; e++) ss += v[gi][e] * v[gi][e];
   }
-  ss = wave_sum(ss);
-  if (lane == 0) red[wv] = ss;
-  __syncthreads();
+  // the delta's norm factor (post_w), then state += delta (times it and post_w)
+  const float dinv = post_w ? 1.f / sqrtf(block_total(ss, red) / (float)n + eps) : 1.f;
   ss = 0.f;
 #pragma unroll
-  for (uint32_t u = 0; u < RN_T / 64; u++) ss += red[u];
-  const float inv = 1.f / sqrtf(ss / (float)n + eps);
+  for (uint32_t gi = 0; gi < RN_G; gi++) {
+    const uint32_t k = 8 * (tid + RN_T * gi);
+    if (k >= n) break;
+    const float4 ha = *(const float4 *)(sr + k), hb = *(const float4 *)(sr + k + 4);
+    const float h[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+    if (post_w) {
+      const float4 pa = *(const float4 *)(post_w + k), pb = *(const float4 *)(post_w + k + 4);
+      const float pw[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[gi][e] = h[e] + v[gi][e] * dinv * pw[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[gi][e] = h[e] + v[gi][e];
+    }
+    *(float4 *)(sr + k) = make_float4(v[gi][0], v[gi][1], v[gi][2], v[gi][3]);
+    *(float4 *)(sr + k + 4) = make_float4(v[gi][4], v[gi][5], v[gi][6], v[gi][7]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += v[gi][e] * v[gi][e];
+  }
+  const float inv = 1.f / sqrtf(block_total(ss, red) / (float)n + eps);
   float *yr = y + (uint64_t)tok * n;
 #pragma unroll
   for (uint32_t gi = 0; gi < RN_G; gi++) {
@@ -180,13 +205,14 @@ hipError_t residual_split(hipStream_t s, const float *part, uint32_t splits, flo
 }
 
 hipError_t reduce_norm_split(hipStream_t s, const float *part, uint32_t splits, float *state, const float *w, float *y,
-                             uint16_t *xs, uint32_t n, float eps, uint32_t batch) {
+                             uint16_t *xs, uint32_t n, float eps, uint32_t batch, const float *post_w) {
   if (!batch) return hipSuccess;
   if (n % SPLIT_K || n > RN_G * 8 * RN_T || !splits || splits > MAX_SPLITS ||
       (uint64_t)splits * n * batch * 4 >= (1ull << 31) ||
-      ((uintptr_t)part | (uintptr_t)state | (uintptr_t)w | (uintptr_t)y) % 16)
+      ((uintptr_t)part | (uintptr_t)state | (uintptr_t)w | (uintptr_t)y | (uintptr_t)post_w) % 16)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_reduce_norm_split, dim3(batch), dim3(RN_T), 0, s, part, splits, state, w, y, xs, n, batch, eps);
+  hipLaunchKernelGGL(k_reduce_norm_split, dim3(batch), dim3(RN_T), 0, s, part, splits, state, post_w, w, y, xs, n,
+                     batch, eps);
   return hipGetLastError();
 }
 
