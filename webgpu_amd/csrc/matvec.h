@@ -11,7 +11,9 @@ namespace wgd {
 // applies it to its dot products after reducing the sums of squares over the whole vector
 // inside each workgroup (every workgroup reads all of K), so no launch needs a
 // cross-workgroup reduction. 16-element blocks let a producer quantize its output in
-// 16-row tiles. Layout in one buffer of qx_bytes(K), Kp = K rounded up to 64:
+// 16-row tiles. Three digits are f32-level; two (x within 1.6e-5 * max|x| of its block)
+// exceed a 1e-3 relative logits bound at the 8B decoder shape. Layout in one buffer of
+// qx_bytes(K), Kp = K rounded up to 64:
 //   d0[Kp] d1[Kp] d2[Kp] | scale[Kp/16] sum[Kp/16] sq[Kp/16]
 struct QXOut {
   int8_t *d0 = nullptr, *d1 = nullptr, *d2 = nullptr;

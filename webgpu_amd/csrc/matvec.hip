@@ -55,10 +55,6 @@ __global__ __launch_bounds__(256) void k_quantize(const float *x, uint32_t K, co
 
 // ------------------------------------------------------------------ chunk kernels
 
-// Activation digits used by the matvec. Two (x within 1.6e-5 * max|x| of its block) exceed
-// a 1e-3 relative logits bound at the 8B decoder shape; three are f32-level.
-constexpr int DIG = 3;
-
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // Weight loads: raw buffer loads over the matrix allocation (a 128-bit resource in SGPRs),
