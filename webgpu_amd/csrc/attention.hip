@@ -924,7 +924,7 @@ __global__ __launch_bounds__(256) void k_attn_dec2(AttnDecK a) {
 }
 
 // Merge of the chunks of one query head: thread d owns output element d. The partials were
-// written by the previous launch (other XCDs' L2). Every load goes out at once, before the
+// written by the previous launch. Every load goes out at once, before the
 // position arrives: raw buffer loads over the head's nsplit partials (zero past them), the
 // first AD_ZB chunks' outputs in registers; chunks at or past the active count are masked
 // afterwards. So the merge is one round trip.
@@ -932,7 +932,7 @@ constexpr uint32_t AD_MAX_SPLITS = 1024, AD_ZB = 32;
 //
 // With group > 0 (kv heads a multiple of 8) workgroup w, dispatched to XCD w % 8, merges a
 // head of a kv head kv with kv % 8 == w % 8: the chunk launch's workgroup z * kv_heads + kv
-// ran on that XCD, so the head's partials were written through its L2.
+// wrote that head's partials on the same XCD.
 __global__ __launch_bounds__(256) void k_attn_comb(const float *part, float *y, QXOut qx, const int32_t *pos_dev,
                                                    uint32_t window, uint32_t chunk, uint32_t nsplit, uint32_t hd,
                                                    uint32_t group) {

@@ -570,8 +570,10 @@ __device__ __forceinline__ void glu_finish8(const float *part, uint32_t splits, 
 // The GEMM's 128-row tile t ran on XCD t % 8 (its grid's first dimension, the tile count, is
 // a multiple of 8, and workgroups go to the XCDs round-robin), and with R a multiple of 1024
 // the up tile of a column has the gate tile's residue. Then (by_xcd) workgroup w, on XCD
-// w % 8, takes token w / 8 and the columns of the tiles t = w (mod 8), reading partials
-// written through its own L2; otherwise workgroup w takes 256 consecutive column groups.
+// w % 8, takes token w / 8 and the columns of the tiles t = w (mod 8), reading only
+// partials its XCD wrote: each 128-row run of the scratch stays with one XCD, and the next
+// GEMM's writes to it take no coherence probes. Otherwise workgroup w takes 256
+// consecutive column groups.
 template <uint32_t S>
 __global__ __launch_bounds__(256) void k_glu_reduce(const float *part, uint32_t splits, uint32_t R, uint32_t batch,
                                                     float *y, uint16_t *xs, int act, DeferredNorm dn, uint32_t by_xcd) {

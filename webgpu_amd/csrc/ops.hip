@@ -155,7 +155,9 @@ __global__ __launch_bounds__(512) void k_reduce_norm_split(const float *part, ui
 // XCD t % 8 (its grid's first dimension is the tile count, a multiple of 8 here, and
 // workgroups are dispatched to the XCDs round-robin). So when n is a multiple of 1024,
 // segment x holds the tiles t = x (mod 8), and workgroup (x, token), dispatched to XCD x,
-// reads partials written through its own L2. Otherwise segment x is elements
+// reads only partials that XCD wrote. Each 128-row run of the scratch then stays with one
+// XCD, so the next GEMM's writes to it find no copy in another XCD's L2 to invalidate
+// (coherence probes, which slow that GEMM). Otherwise segment x is elements
 // [RS_E x, RS_E (x + 1)).
 constexpr uint32_t RS_T = 128, RS_E = 8 * RS_T;
 static bool residual_by_xcd(uint32_t n) { return n % 1024 == 0; }
@@ -408,7 +410,8 @@ hipError_t rope_table(hipStream_t s, float2 *cs, uint32_t rot, uint32_t n, uint3
 // With hd 128 and a multiple of 8 head slots (by_xcd), slot s is the GEMM's 128-row tile s,
 // which ran on XCD s % 8 (the tile count leads its grid; workgroups go to the XCDs
 // round-robin). Workgroup w, on XCD w % 8, then takes slots s = w (mod 8), so it reads
-// partials written through its own L2; otherwise workgroup w takes items 4w .. 4w + 3.
+// only partials its XCD wrote and the next GEMM's writes to the scratch take no coherence
+// probes; otherwise workgroup w takes items 4w .. 4w + 3.
 __global__ __launch_bounds__(256) void k_qkv_finish(QKVFinish a, uint32_t by_xcd) {
   __shared__ float buf[4][512];
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
