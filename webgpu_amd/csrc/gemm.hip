@@ -646,6 +646,22 @@ static uint32_t group_kspan(const GemmGroup &g, uint32_t batch, uint64_t scratch
   const uint32_t units = cols / align;
   if (splits > units) splits = units;
   if (splits > 16) splits = 16;
+  // The workgroups run in rounds of `target` slots, and a short last round leaves CUs idle
+  // (336 gate/up tiles in one split fill 66% of one round). Up to twice the splits are
+  // considered, and one that fills its rounds at least 10 points better is taken: 336 tiles
+  // then run in 3 splits, 1008 workgroups in two rounds at 98%. The split count is
+  // ceil(units / per) for the span per = ceil(units / s).
+  auto workgroups = [&](uint32_t s) {
+    const uint32_t per = (units + s - 1) / s;
+    return (uint64_t)tiles * ((units + per - 1) / per);
+  };
+  auto rounds = [&](uint64_t wg) { return (wg + target - 1) / target; };
+  uint64_t bw = workgroups(splits);
+  for (uint32_t s = splits + 1; s <= 2 * splits + 1 && s <= units && s <= 16; s++) {
+    const uint64_t w = workgroups(s);
+    // w / (rounds(w) T) > bw / (rounds(bw) T) + 0.1, times 10 rounds(w) rounds(bw) T
+    if (10 * w * rounds(bw) > 10 * bw * rounds(w) + rounds(w) * rounds(bw) * target) { splits = s; bw = w; }
+  }
   while (splits > 1 && (uint64_t)splits * batch * rows > scratch_floats) splits--;
   const uint32_t per = (units + splits - 1) / splits;
   return per * align;
