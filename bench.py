@@ -54,17 +54,20 @@ PEAK_HBM = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mv_matvec_microbench.md")
 
 
-# The sources of the roofline kernel; the counter summary records their digest, so a line whose
-# traffic comes from a profile of another version of the kernel says so.
+# The sources of the roofline kernel and its file's own build flags; the counter summary records
+# their digest, so a line whose traffic comes from a profile of another version of the kernel
+# says so.
 KERNEL_SOURCES = [os.path.join(ROOT, "webgpu_amd", "csrc", f) for f in ("matvec.hip", "matvec.h", "decode.h")]
 
 
 def kernel_source_digest() -> str:
     import hashlib
+    from webgpu_amd.build import FILE_FLAGS
     h = hashlib.sha256()
     for path in KERNEL_SOURCES:
         with open(path, "rb") as fh:
             h.update(fh.read())
+    h.update(" ".join(FILE_FLAGS.get("matvec.hip", [])).encode())
     return h.hexdigest()[:16]
 
 

@@ -24,11 +24,16 @@ FLAGS = [
     "-Wall", "-Wno-unused-value", "-Wno-pass-failed", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
     "-I" + os.path.join(HERE, "..", "include"),
 ]
+# The decode matvec waits on its weight loads for about half of a wavefront's life. LLVM's
+# memory-clause scheduling strategy groups those loads, which makes the 14336x4096 Q4_K
+# launch 3.6% faster and the Q6_K head 2.6% faster. Scheduling reorders no floating-point
+# arithmetic, so the results are the same bits.
+FILE_FLAGS = {"matvec.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
