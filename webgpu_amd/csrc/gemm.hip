@@ -657,7 +657,8 @@ static uint32_t group_kspan(const GemmGroup &g, uint32_t batch, uint64_t scratch
   };
   auto rounds = [&](uint64_t wg) { return (wg + target - 1) / target; };
   uint64_t bw = workgroups(splits);
-  for (uint32_t s = splits + 1; s <= 2 * splits + 1 && s <= units && s <= 16; s++) {
+  const uint32_t s0 = splits;
+  for (uint32_t s = s0 + 1; s <= 2 * s0 + 1 && s <= units && s <= 16; s++) {
     const uint64_t w = workgroups(s);
     // w / (rounds(w) T) > bw / (rounds(bw) T) + 0.1, times 10 rounds(w) rounds(bw) T
     if (10 * w * rounds(bw) > 10 * bw * rounds(w) + rounds(w) * rounds(bw) * target) { splits = s; bw = w; }
