@@ -153,10 +153,13 @@ def test_widths_outside_the_planar_tiles_stay_in_the_gguf_layout(gpu, type_):
 
 @pytest.mark.parametrize("type_,rows,cols,batch", [(Q4_K, 4096, 4096, 128), (Q6_K, 1024, 4096, 130),
                                                    (Q8_0, 384, 2048, 128), (Q4_K, 640, 14336, 64),
-                                                   (Q5_K, 1024, 4096, 128), (Q4_0, 512, 4096, 130)])
+                                                   (Q5_K, 1024, 4096, 128), (Q4_0, 512, 4096, 130),
+                                                   (Q4_K, 33280, 1024, 64)])
 def test_prompt_gemm_real_shapes(gpu, type_, rows, cols, batch):
     """Planar prompt GEMM at layer shapes: whole 128-token tiles, a second token tile,
-    split-K partial sums, a row offset inside a wider output (stride/rowBase, verify.ts:16-38)."""
+    split-K partial sums, a row offset inside a wider output (stride/rowBase, verify.ts:16-38).
+    33280 rows are 260 row tiles, which one K split would run at half of the chip's two
+    workgroups per CU; they take 3 splits, 780 workgroups, and a three-way partial sum."""
     rng = np.random.default_rng(rows * 3 + cols + batch)
     gen = GEN[type_]
     w = gen(rng, rows * cols // QUANTS[type_]["block"])
